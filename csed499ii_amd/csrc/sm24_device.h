@@ -1,0 +1,98 @@
+// Device-side building blocks of the 2:4 INT4 x FP16 GEMM for gfx950 (CDNA4).
+//
+// Operand layouts are the Sparse-Marlin pack() layouts (reference:
+// kernel_experiments/sparse_marlin/src/marlin/__init__.py:331-388), consumed as they
+// lie in HBM:
+//   * B      int32 [K/32][2N]: nibble p of word (r, 128*c + 4*i + j) is the offset-8
+//            code of compressed-K row 16r + ROW_t[p] (t = i%4) and output column
+//            64c + 8*(i/4) + 4*BLK[p] + j, ROW_t = {2t,2t+8,2t,2t+8,2t+1,2t+9,2t+1,2t+9},
+//            BLK = {0,0,1,1,0,0,1,1}.
+//   * meta   int16, CUTLASS-reordered (reference _semi_structured_conversions.py:21-48):
+//            for k-block r and 64-column chunk c the 256 bytes at int16 offset
+//            2N*r + 128*c hold 32 units of 4 int16; unit q = 16*(j>>1) + 2*g + (j&1)
+//            is {m(n,e0), m(n+4,e0), m(n,e1), m(n+4,e1)} for n = 64c + 8g + j, where
+//            e selects the first/second 16 dense K of the k-block and nibble u of an
+//            int16 is the 2:4 pattern (idx0 | idx1 << 2) of dense group u.
+//   * s      fp16 [K/128][N] grouped (within 64 columns, packed slot 8a+b holds
+//            column 8a + {0,4,1,5,2,6,3,7}[b]) or [1][N] per column (natural order).
+//
+// Sparse MFMA operand layout on gfx950, measured on the device (one-hot/random
+// probes against a CPU model):
+//   v_smfmac_f32_16x16x32_f16: A lane l: row l%16, 4 halves = 2 dense groups
+//     (k-space groups 2*(l/16), 2*(l/16)+1), index byte ABID of the idx VGPR holds
+//     (idx0 | idx1<<2) per group; B lane l: column l%16, k-space 8*(l/16)+[0,8);
+//     D lane l: rows 4*(l/16)+[0,4), column l%16.
+//   v_smfmac_f32_16x16x64_f16: A lane l: row l%16, 8 halves = k-space groups
+//     4*(l/16)+[0,4), index half-word ABID; B lane l: column l%16, k-space
+//     8*(l/16)+[0,8) then 32+8*(l/16)+[0,8); D as above.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sm24 {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half16_t __attribute__((ext_vector_type(16)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// 8-byte load from an address that is only 4-byte aligned (3-bit value stream).
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Codes of one output column held in a packed word (after ">> 8" for the second
+// column of the pair), as the four halves of a 16x16x32 A operand:
+// {code(p0), code(p4), code(p1), code(p5)} - 8, exact in fp16.
+// Magic-exponent conversion: (q & 0x000f000f) | 0x6400 is 1024 + code, and the
+// high nibble pair is 1024 + 16*code, scaled by 1/16 and shifted by -72.
+__device__ __forceinline__ half4_t dequant4(uint32_t q) {
+  const uint32_t lo = (q & 0x000F000Fu) | 0x64006400u;
+  const uint32_t hi = (q & 0x00F000F0u) | 0x64006400u;
+  const half2_t l = __builtin_bit_cast(half2_t, lo) - (half2_t){(_Float16)1032.0f, (_Float16)1032.0f};
+  const half2_t h = __builtin_bit_cast(half2_t, hi) * (half2_t){(_Float16)0.0625f, (_Float16)0.0625f} +
+                    (half2_t){(_Float16)-72.0f, (_Float16)-72.0f};
+  return (half4_t){l.x, l.y, h.x, h.y};
+}
+
+// Same for 3-bit codes (zero point 4) already spread to nibble positions.
+__device__ __forceinline__ half4_t dequant3(uint32_t q) {
+  const uint32_t lo = (q & 0x000F000Fu) | 0x64006400u;
+  const uint32_t hi = (q & 0x00F000F0u) | 0x64006400u;
+  const half2_t l = __builtin_bit_cast(half2_t, lo) - (half2_t){(_Float16)1028.0f, (_Float16)1028.0f};
+  const half2_t h = __builtin_bit_cast(half2_t, hi) * (half2_t){(_Float16)0.0625f, (_Float16)0.0625f} +
+                    (half2_t){(_Float16)-68.0f, (_Float16)-68.0f};
+  return (half4_t){l.x, l.y, h.x, h.y};
+}
+
+// Spread 8 three-bit codes (bits 3i..3i+2 of a 24-bit field) to nibble i.
+__device__ __forceinline__ uint32_t spread3(uint32_t x) {
+  x = ((x & 0x00FFF000u) << 4) | (x & 0x00000FFFu);
+  x = ((x & 0x0FC00FC0u) << 2) | (x & 0x003F003Fu);
+  return ((x & 0x38383838u) << 1) | (x & 0x07070707u);
+}
+
+__device__ __forceinline__ half4_t scale4(half4_t a, _Float16 s) {
+  return a * (half4_t){s, s, s, s};
+}
+
+// Sparse-index bytes for one unit pair: d0 = {m(n,e0) | m(n+4,e0) << 16},
+// d1 = {m(n,e1) | m(n+4,e1) << 16}; sh = 4*h selects dense groups h and h+4.
+// Result byte 0: index byte of column n, byte 2: of column n+4.
+__device__ __forceinline__ uint32_t idx_pair(uint32_t d0, uint32_t d1, uint32_t sh) {
+  const uint32_t x = (d0 >> sh) & 0x000F000Fu;
+  const uint32_t y = (d1 >> sh) & 0x000F000Fu;
+  return x | (y << 4);
+}
+
+template <int ABID>
+__device__ __forceinline__ float4_t smfmac32(half4_t a, half8_t b, float4_t c, uint32_t idx) {
+  return __builtin_amdgcn_smfmac_f32_16x16x32_f16(a, b, c, (int)idx, 0, ABID);
+}
+
+template <int ABID>
+__device__ __forceinline__ float4_t smfmac64(half8_t a, half16_t b, float4_t c, uint32_t idx) {
+  return __builtin_amdgcn_smfmac_f32_16x16x64_f16(a, b, c, (int)idx, 0, ABID);
+}
+
+}  // namespace sm24

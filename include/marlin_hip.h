@@ -1,0 +1,96 @@
+/* C ABI of the MI355X (gfx950) Sparse-Marlin 2:4 INT4 x FP16 GEMM library
+ * (libmarlin_hip.so).  Plain pointers and sizes only; every tensor is caller-owned
+ * device memory on device `dev`, and every call is asynchronous on `stream`.
+ *
+ * Naming follows the reference: prob_m = N (output features), prob_n = batch rows
+ * M, prob_k = K; groupsize is in COMPRESSED-K units (64 for a dense group of 128,
+ * -1 for one scale per output column).
+ *
+ * Return codes mirror the reference dispatch (marlin_cuda_kernel_nm.cu:748-749):
+ *   0 ok, 1 problem shape incompatible with the tile, 2 no kernel for the tile or
+ *   group size, and 3 (new) a HIP launch or scratch-allocation failure, described
+ *   by marlin_hip_last_error().
+ *
+ * Buffer sizes are the caller's contract (they cannot be checked through plain
+ * pointers): A M*K halves, B K*N/16 int32, meta K*N/16 int16, C M*N halves,
+ * s (K/128 or 1)*N halves.
+ *
+ * Split-K scratch (fp32 partials and arrival counters) is allocated by the library
+ * once per device, grown on demand outside stream capture, and shared by all
+ * streams: GEMM calls that overlap in time on one device race (serialise them on
+ * one stream, as with the reference's shared workspace).  The counters carry a
+ * per-launch tag, so no buffer needs to be zeroed by the caller.
+ */
+#ifndef MARLIN_HIP_H
+#define MARLIN_HIP_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MARLIN_HIP_OK = 0,
+  MARLIN_HIP_ERR_PROB_SHAPE = 1,
+  MARLIN_HIP_ERR_KERN_SHAPE = 2,
+  MARLIN_HIP_ERR_LAUNCH = 3
+};
+
+/* C[M,N] = A[M,K] * W[K,N], W in the Sparse-Marlin pack() layout.
+ * Replaces marlin::marlin_cuda_2_4 (kernel_experiments/sparse_marlin/src/marlin/
+ * marlin_cuda_kernel_nm.cu:751-755), same parameter order and meaning.
+ * `workspace` and `max_par` are accepted for signature compatibility; this library
+ * keeps its own zero-initialised scratch, so the caller's workspace need not be
+ * zeroed.  thread_k/thread_m are validated exactly as the reference does. */
+int marlin_hip_mul_2_4(const void* A, const void* B, const void* meta, void* C, void* s,
+                       int prob_m, int prob_n, int prob_k, void* workspace, int groupsize,
+                       int dev, hipStream_t stream, int thread_k, int thread_m, int sms,
+                       int max_par);
+
+/* Same GEMM with 3-bit-compressed metadata (48 uint32 per 64-word group) as
+ * produced by marlin_hip_meta3_pack.  Replaces the generated
+ * decode_fetch::marlin_cuda_2_4 (kernel_experiments/sparse_marlin/metadata_decode/
+ * setup.py:13-44, bound at setup.py:36-44). */
+int marlin_hip_mul_2_4_meta3(const void* A, const void* B, const void* meta3, void* C, void* s,
+                             int prob_m, int prob_n, int prob_k, void* workspace, int groupsize,
+                             int dev, hipStream_t stream, int thread_k, int thread_m, int sms,
+                             int max_par);
+
+/* Same GEMM with 3-bit nonzero values: B3 is the code stream of the 4-bit layout
+ * re-packed at 3 bits per code (code of nibble p of word w at bit 3*(8w+p), the
+ * kernel_experiments/3bit_encoding bit layout), codes offset by 4.  The reference
+ * has no implementation of 3-bit values (its 3-bit work encodes metadata); this
+ * entry point serves the BASELINE config that asks for them. */
+int marlin_hip_mul_2_4_w3(const void* A, const void* B3, const void* meta, void* C, void* s,
+                          int prob_m, int prob_n, int prob_k, void* workspace, int groupsize,
+                          int dev, hipStream_t stream, int thread_k, int thread_m, int sms,
+                          int max_par);
+
+/* 4-bit 2:4 metadata (n_int16 int16, multiple of 128) -> 3-bit codes
+ * (n_int16*3/8 uint32).  `errors` is a device uint32 counter that is incremented
+ * once per nibble that is not a valid 2:4 pattern (the caller zeroes it).
+ * Replaces pack_metadata (kernel_experiments/sparse_marlin/metadata_decode/
+ * codec.cu:18-24, 30-35). */
+int marlin_hip_meta3_pack(const void* meta, void* out, long long n_int16, void* errors,
+                          int dev, hipStream_t stream);
+
+/* Inverse of marlin_hip_meta3_pack: n_words uint32 (multiple of 48) -> n_words*8/3
+ * int16.  Replaces unpack_metadata (codec.cu:25-29, 36-41). */
+int marlin_hip_meta3_unpack(const void* packed, void* out, long long n_words, int dev,
+                            hipStream_t stream);
+
+/* Expand n_groups groups of 128 three-bit codes (48 bytes each, code i at bit 3i)
+ * into 128 nibbles (64 bytes each) with dec(x) = {4,4,9,8,E,E,D,C}[x].
+ * Replaces expansion<9> (kernel_experiments/3bit_encoding/experiment.cu:36-40). */
+int marlin_hip_expand3(const void* in, void* out, long long n_groups, int dev,
+                       hipStream_t stream);
+
+/* Message describing the last MARLIN_HIP_ERR_* of the calling thread. */
+const char* marlin_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MARLIN_HIP_H */

@@ -1,0 +1,190 @@
+"""GPU parity of the 2:4 INT4 GEMM (libmarlin_hip.so via the C ABI) against the
+CPU oracle, on the reference's own test shapes (test_2_4.py:91-135, run.py:46),
+ragged batches, the BASELINE shapes (checked through 256-column slices at full K),
+determinism, full overwrite of C and hipGraph replay."""
+import numpy as np
+import pytest
+import torch
+
+from csed499ii_amd import marlin, synth
+from tests.gpu_util import assert_close, oracle_gemm, slice_cols, to_cpu
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _problem(M, N, K, g, seed, bits=4):
+    wt = synth.make_weight(K, N, seed, g, bits=bits, device=DEV)
+    A = synth.make_activation(M, K, seed, device=DEV)
+    return wt, A
+
+
+def _run(wt, A, fn=None, thread_k=-1, thread_m=-1, meta=None):
+    fn = fn or (marlin.mul_2_4 if wt["bits"] == 4 else marlin.mul_2_4_w3)
+    M, N = A.shape[0], wt["N"]
+    C = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    ws = torch.zeros(max(N // 128 * 16, 16), dtype=torch.int32, device=DEV)
+    fn(A, wt["B"], wt["meta"] if meta is None else meta, C, wt["s"], ws, thread_k, thread_m)
+    torch.cuda.synchronize()
+    return C
+
+
+def _check(wt, A, C, what):
+    t = to_cpu(wt)
+    ref = oracle_gemm(A.cpu().numpy(), t)
+    return assert_close(C.cpu().numpy(), ref, what)
+
+
+def test_reference_correctness_cases():
+    """test_2_4.py:91-93: (N, batch, K) = (256, 16, 256) g=-1 tile 128x128 and
+    (21504, 16, 4096) g=128 tile 64x256 (the latter checked on column slices)."""
+    wt, A = _problem(16, 256, 256, -1, 1)
+    C = _run(wt, A, thread_k=128, thread_m=128)
+    _check(wt, A, C, "256x16x256")
+    wt, A = _problem(16, 21504, 4096, 128, 2)
+    C = _run(wt, A, thread_k=64, thread_m=256)
+    t = to_cpu(wt)
+    for c0 in (0, 160, 332):
+        ts = slice_cols(t, c0, 4)
+        ref = oracle_gemm(A.cpu().numpy(), ts)
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"21504 slice {c0}")
+    assert torch.isfinite(C).all()
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8, 12, 16, 32, 64])
+@pytest.mark.parametrize("tile", [(64, 256), (128, 128)])
+def test_reference_tiles(batch, tile):
+    """test_2_4.py:95-101 (N=512, K=1024, g=-1)."""
+    if batch > 16 and tile == (128, 128):
+        pytest.skip("the reference has no 128x128 kernel for more than one batch block")
+    wt, A = _problem(batch, 512, 1024, -1, 10 + batch)
+    C = _run(wt, A, thread_k=tile[0], thread_m=tile[1])
+    _check(wt, A, C, f"tiles batch={batch} {tile}")
+
+
+@pytest.mark.parametrize("K", [768, 832, 896])
+def test_reference_k_stages(K):
+    """test_2_4.py:103-106."""
+    wt, A = _problem(16, 512, K, -1, K)
+    _check(wt, A, _run(wt, A, thread_k=64, thread_m=256), f"K={K}")
+
+
+@pytest.mark.parametrize("K", [64, 128, 192])
+def test_reference_very_few_stages(K):
+    """test_2_4.py:108-111 (N=768)."""
+    wt, A = _problem(16, 768, K, -1, K + 1)
+    _check(wt, A, _run(wt, A, thread_k=64, thread_m=256), f"K={K}")
+
+
+@pytest.mark.parametrize("N,K", [(256, 512), (256, 1024), (256 * 128, 1024)])
+@pytest.mark.parametrize("tile", [(128, 128), (64, 256)])
+def test_reference_groups(N, K, tile):
+    """test_2_4.py:129-135 (batch 16, g=128)."""
+    wt, A = _problem(16, N, K, 128, N + K)
+    C = _run(wt, A, thread_k=tile[0], thread_m=tile[1])
+    if N <= 4096:
+        _check(wt, A, C, f"groups {N}x{K}")
+    else:
+        t = to_cpu(wt)
+        for c0 in (0, 255, 508):
+            ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+            assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"groups slice {c0}")
+
+
+@pytest.mark.parametrize("M", [1, 16, 32])
+@pytest.mark.parametrize("g", [-1, 128])
+def test_run_py_check_cases(M, g):
+    """run.py:46 (N=512, K=1024)."""
+    wt, A = _problem(M, 512, 1024, g, 100 + M)
+    _check(wt, A, _run(wt, A), f"M={M} g={g}")
+
+
+@pytest.mark.parametrize("M", [3, 7, 17, 33, 50, 100, 129])
+def test_ragged_batches(M):
+    wt, A = _problem(M, 1024, 2048, 128, 200 + M)
+    _check(wt, A, _run(wt, A), f"M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_config1_and_decode_o_proj(M):
+    """BASELINE config 1 (M=16) and the decode sweep at the O-projection shape."""
+    wt, A = _problem(M, 4096, 4096, 128, 20261019 + M)
+    _check(wt, A, _run(wt, A), f"4096^2 M={M}")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 22016), (11008, 4096)])
+@pytest.mark.parametrize("M", [1, 16])
+def test_decode_sweep_full_size_slices(K, N, M):
+    wt, A = _problem(M, N, K, 128, K + N + M)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2 - 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"{K}x{N} M={M} slice {c0}")
+
+
+@pytest.mark.parametrize("M", [512])
+def test_prefill_shape_slices(M):
+    wt, A = _problem(M, 8192, 8192, 128, 31)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    t = to_cpu(wt)
+    for c0 in (0, 64, 124):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"prefill M={M} slice {c0}")
+
+
+def test_deterministic_repeats():
+    """Split-K reductions run in a fixed order: repeated calls are bit-identical
+    (the reference's variant smoke test demands identical repeats)."""
+    for M, N, K in ((1, 4096, 4096), (16, 1024, 11008), (48, 2048, 4096)):
+        wt, A = _problem(M, N, K, 128, 7)
+        outs = [_run(wt, A) for _ in range(3)]
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_graph_replay_matches_eager():
+    wt, A = _problem(8, 4096, 4096, 128, 9)
+    ws = torch.zeros(4096 // 128 * 16, dtype=torch.int32, device=DEV)
+    C_eager = torch.empty(8, 4096, dtype=torch.half, device=DEV)
+    marlin.mul_2_4(A, wt["B"], wt["meta"], C_eager, wt["s"], ws)
+    torch.cuda.synchronize()
+    C = torch.zeros(8, 4096, dtype=torch.half, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(3):
+            marlin.mul_2_4(A, wt["B"], wt["meta"], C, wt["s"], ws)
+    for _ in range(4):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, C_eager)
+
+
+def test_layer_forward():
+    K, N = 1024, 512
+    gen = torch.Generator().manual_seed(3)
+    w = (torch.randn((K, N), generator=gen) * 0.02).half().to(DEV)
+    q, s, ref = synth.quantize(w, 128)
+    layer = marlin.Layer_2_4(K, N, groupsize=128).to(DEV)
+    lin = torch.nn.Linear(K, N)
+    lin.weight.data = ref
+    layer.pack(lin, s, True)
+    x = torch.randn((2, 3, K), generator=gen).half().to(DEV)
+    y = layer(x)
+    assert y.shape == (2, 3, N)
+    t = {"B": layer.B.cpu().numpy(), "meta": layer.meta.cpu().numpy(), "s": layer.s.cpu().numpy(),
+         "K": K, "N": N, "groupsize": 128, "bits": 4}
+    refc = oracle_gemm(x.reshape(6, K).cpu().numpy(), t)
+    assert_close(y.reshape(6, N).cpu().numpy(), refc, "Layer_2_4.forward")
+
+
+def test_kernel_shape_errors_raise():
+    wt, A = _problem(32, 512, 1024, -1, 5)
+    with pytest.raises(RuntimeError, match="No kernel implementation for thread_k=128, thread_m=128"):
+        _run(wt, A, thread_k=128, thread_m=128)
+    with pytest.raises(RuntimeError, match=r"Problem \(m=512, n=32, k=1024\) not compatible"):
+        _run(wt, A, thread_k=64, thread_m=384)

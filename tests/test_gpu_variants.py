@@ -1,0 +1,99 @@
+"""GPU parity of the 3-bit variants: the 3-bit metadata codec and GEMM (reference
+metadata_decode experiment), the 3-bit code expansion (3bit_encoding experiment),
+and the 3-bit nonzero-value GEMM of BASELINE config 4."""
+import numpy as np
+import pytest
+import torch
+
+from csed499ii_amd import marlin, synth
+from oracle import sm24_oracle as o
+from tests.gpu_util import assert_close, oracle_gemm, slice_cols, to_cpu
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _ws(N):
+    return torch.zeros(max(N // 128 * 16, 16), dtype=torch.int32, device=DEV)
+
+
+@pytest.mark.parametrize("K,N", [(1024, 512), (4096, 4096)])
+def test_meta3_codec_bit_exact(K, N):
+    wt = synth.make_weight(K, N, 5, 128, device=DEV)
+    packed = marlin.pack_meta3(wt["meta"].reshape(-1))
+    ref, bad = o.meta3_pack(wt["meta"].cpu().numpy())
+    assert bad == 0
+    assert packed.numel() == wt["meta"].numel() * 3 // 8
+    assert np.array_equal(packed.cpu().numpy().view(np.uint32), ref)
+    back = marlin.unpack_meta3(packed)
+    assert torch.equal(back, wt["meta"].reshape(-1))
+
+
+def test_meta3_rejects_invalid_nibbles():
+    meta = torch.full((256,), 0x4444, dtype=torch.int16, device=DEV)
+    meta[17] = 0x4443
+    with pytest.raises(RuntimeError, match="unsupported 2:4 nibbles"):
+        marlin.pack_meta3(meta)
+
+
+@pytest.mark.parametrize("M,N,K,g", [(1, 4096, 4096, 128), (16, 4096, 4096, 128), (48, 1024, 2048, -1),
+                                     (16, 12288, 4096, 128)])
+def test_meta3_gemm_equals_baseline_bit_exact(M, N, K, g):
+    """Same arithmetic, compressed metadata: outputs must be identical."""
+    wt = synth.make_weight(K, N, M + N, g, device=DEV)
+    A = synth.make_activation(M, K, 3, device=DEV)
+    packed = marlin.pack_meta3(wt["meta"].reshape(-1))
+    C0 = torch.empty(M, N, dtype=torch.half, device=DEV)
+    C1 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    marlin.mul_2_4(A, wt["B"], wt["meta"], C0, wt["s"], _ws(N))
+    marlin.mul_2_4_meta3(A, wt["B"], packed, C1, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    assert torch.equal(C0, C1)
+    if N <= 4096:
+        assert_close(C1.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), "meta3")
+
+
+@pytest.mark.parametrize("M", [1, 16, 256])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 12288), (11008, 4096)])
+def test_w3_gemm_config4(M, K, N):
+    """3-bit values, Llama-2-7B shapes, M in {1, 16, 256}."""
+    wt = synth.make_weight(K, N, 4 + K + N, 128, bits=3, device=DEV)
+    A = synth.make_activation(M, K, 4, device=DEV)
+    C = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    assert torch.isfinite(C).all()
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"w3 {K}x{N} M={M} slice {c0}")
+
+
+def test_w3_gemm_small_full_oracle():
+    for M, N, K, g in ((5, 512, 1024, -1), (16, 768, 192, -1), (33, 1024, 2048, 128)):
+        wt = synth.make_weight(K, N, M, g, bits=3, device=DEV)
+        A = synth.make_activation(M, K, M, device=DEV)
+        C = torch.empty(M, N, dtype=torch.half, device=DEV)
+        marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C, wt["s"], _ws(N))
+        torch.cuda.synchronize()
+        assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), f"w3 {M}x{N}x{K}")
+
+
+def test_expand3_exhaustive():
+    """All 2^24 packed 8-code inputs (3bit_encoding/experiment.cu:70, 84)."""
+    x = np.arange(1 << 24, dtype=np.uint32)
+    stream = np.stack([x & 255, (x >> 8) & 255, (x >> 16) & 255], axis=-1).astype(np.uint8).ravel()
+    got = marlin.expand3(torch.from_numpy(stream).to(DEV))
+    torch.cuda.synchronize()
+    ref = o.expand3(stream)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref)
+
+
+@pytest.mark.parametrize("groups", [1, 2, 3, 7, 9, 31, 33])
+def test_expand3_partial_blocks(groups):
+    """Group counts that leave partial thread blocks (experiment.cu:87)."""
+    rng = np.random.default_rng(groups)
+    stream = rng.integers(0, 256, size=48 * groups, dtype=np.uint8)
+    got = marlin.expand3(torch.from_numpy(stream).to(DEV))
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), o.expand3(stream))
