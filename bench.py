@@ -1,0 +1,308 @@
+"""Benchmark of the MI355X 2:4 INT4 x FP16 GEMM (libmarlin_hip.so).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|w3|meta3|stack]
+
+Default workload (BASELINE config "decode sweep"): Llama-2-7B projection shapes
+(K x N = 4096x12288 QKV, 4096x4096 O, 4096x22016 gate/up, 11008x4096 down) at batch
+M in {1, 2, 4, 8, 16}, 2:4 INT4 weights with group-128 fp16 scales.  One step is one
+pass over the 20 (shape, M) calls, captured once in a HIP graph and replayed; the
+weights rotate through copies totalling more than the 256 MB Infinity Cache so every
+call streams its weight from HBM.  Prints ONE JSON line; ``value`` is the achieved
+HBM bandwidth on algorithmic compressed-weight bytes (25/64*K*N per call).
+
+Other workloads: ``prefill`` (Llama-2-70B shapes, M in {512..4096}, TFLOP/s),
+``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
+``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+from csed499ii_amd import _lib, marlin, synth
+
+METRIC = "µs/call + achieved HBM GB/s (M=1–16) and TFLOP/s (M≥512), 2:4 INT4 GEMM"
+HBM_PEAK_GBS = 8000.0
+SPARSE_F16_PEAK_TFLOPS = 5000.0  # dense-equivalent FLOPs of 2:4 fp16 MFMA (2.5 PFLOP/s dense)
+MALL_BYTES = 256 << 20
+
+LLAMA7B = [("qkv", 4096, 12288), ("o", 4096, 4096), ("gate_up", 4096, 22016), ("down", 11008, 4096)]
+LLAMA70B = [("qkv", 8192, 10240), ("o", 8192, 8192), ("gate_up", 8192, 57344), ("down", 28672, 8192)]
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class WeightSet:
+    """Copies of one packed weight, handed out round-robin to every call site that
+    uses the shape, so that consecutive uses of one copy are separated by more
+    bytes than the Infinity Cache holds."""
+
+    def __init__(self, copies):
+        self.copies = copies
+        self.i = 0
+
+    def next(self):
+        w = self.copies[self.i % len(self.copies)]
+        self.i += 1
+        return w
+
+
+class Call:
+    """One GEMM call site."""
+
+    def __init__(self, name, K, N, M, wset, A, fn, meta_key="meta"):
+        self.name, self.K, self.N, self.M = name, K, N, M
+        self.wset = wset
+        self.A = A
+        self.C = torch.empty((M, N), dtype=torch.half, device=A.device)
+        self.ws = torch.zeros(N // 128 * 16, dtype=torch.int32, device=A.device)
+        self.fn = fn
+        self.meta_key = meta_key
+        self.bits = wset.copies[0]["bits"]
+
+    def __call__(self):
+        w = self.wset.next()
+        self.fn(self.A, w["B"], w[self.meta_key], self.C, w["s"], self.ws)
+
+    @property
+    def wbytes(self):
+        b = synth.weight_bytes(self.K, self.N, self.bits, 128)
+        if self.meta_key == "meta3":
+            b -= self.K * self.N // 8 // 4  # metadata is 3/4 of the 4-bit size
+        return b
+
+    @property
+    def flops(self):
+        return 2 * self.M * self.K * self.N
+
+
+def make_copies(K, N, seed, bits, copies, device, meta3=False) -> WeightSet:
+    base = synth.make_weight(K, N, seed, 128, bits=bits, device=device)
+    if meta3:
+        base["meta3"] = marlin.pack_meta3(base["meta"].reshape(-1))
+    out = [base]
+    for _ in range(copies - 1):
+        out.append({k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in base.items()})
+    return WeightSet(out)
+
+
+def copies_for(K, N, bits) -> int:
+    """Copies of one weight whose total exceeds the Infinity Cache by 25 %."""
+    return max(2, -(-int(MALL_BYTES * 1.25) // synth.weight_bytes(K, N, bits, 128)))
+
+
+def graph_of(calls, reps=1):
+    """Capture ``reps`` passes over ``calls`` into one graph (after an eager warm-up
+    that sizes the library's scratch)."""
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, replays: int) -> float:
+    """Median-free GPU time (ms) of ``replays`` back-to-back replays, HIP events on the
+    stream the graph launches on."""
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        g.replay()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end)
+
+
+def per_call_stats(calls, samples=5, reps=20):
+    """µs/call of every call site alone: a graph of ``reps`` calls (weights rotating),
+    median over ``samples`` replays."""
+    out = []
+    for c in calls:
+        g = graph_of([c], reps=reps)
+        g.replay()
+        ts = [time_graph(g, 1) * 1000.0 / reps for _ in range(samples)]
+        us = statistics.median(ts)
+        row = {"name": c.name, "M": c.M, "K": c.K, "N": c.N, "us": round(us, 3),
+               "GBps": round(c.wbytes / (us * 1e3), 1)}
+        if c.M >= 256:
+            row["TFLOPs"] = round(c.flops / (us * 1e6), 1)
+        out.append(row)
+        del g
+    return out
+
+
+def cpu_baseline(sample_shape=("o", 4096, 4096), Ms=(1, 16), reps=3):
+    """The oracle (numpy) on the host cores: one-time unpack + dequantize, then fp32
+    matmul (median of ``reps``), as GB/s of algorithmic compressed-weight bytes."""
+    import numpy as np
+
+    from oracle import sm24_oracle as o
+
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    except Exception:  # pragma: no cover - informational only
+        cores = os.cpu_count() or 1
+    name, K, N = sample_shape
+    wt = synth.make_weight(K, N, synth.SEED_BASE + 1, 128, device="cpu")
+    B, meta, s = wt["B"].numpy(), wt["meta"].numpy(), wt["s"].numpy()
+    t0 = time.perf_counter()
+    W = o.dequant(B, meta, s, K, N, 128)
+    t_dq = time.perf_counter() - t0
+    W32 = W.astype(np.float32)
+    rows = {}
+    for M in Ms:
+        A = synth.make_activation(M, K, synth.SEED_BASE, device="cpu").numpy().astype(np.float32)
+        A @ W32  # warm-up
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            A @ W32
+            ts.append(time.perf_counter() - t0)
+        rows[M] = statistics.median(ts)
+    wbytes = synth.weight_bytes(K, N, 4, 128)
+    M_main = max(Ms)
+    value = wbytes / rows[M_main] / 1e9
+    sample = (f"oracle on {name} {K}x{N} g128: dequant {t_dq:.2f} s once; fp32 matmul median of {reps}: "
+              + ", ".join(f"M={m} {rows[m] * 1e3:.2f} ms" for m in Ms) + f"; value at M={M_main}")
+    return {"value": round(value, 3), "unit": "GB/s", "cores": int(cores), "kind": "port", "sample": sample,
+            "us_per_call": {str(m): round(rows[m] * 1e6, 1) for m in Ms}, "dequant_s": round(t_dq, 3)}
+
+
+def build_workload(args, device):
+    wl = args.workload
+    calls = []
+    if wl in ("decode", "meta3", "w3"):
+        shapes = LLAMA7B
+        Ms = [1, 2, 4, 8, 16] if wl != "w3" else [1, 16, 256]
+        bits = 3 if wl == "w3" else 4
+        weights = {}
+        copies = {}
+        for i, (name, K, N) in enumerate(shapes):
+            copies[name] = copies_for(K, N, bits)
+            weights[name] = make_copies(K, N, synth.SEED_BASE + 1 + i, bits, copies[name], device,
+                                        meta3=(wl == "meta3"))
+        fn = marlin.mul_2_4_w3 if wl == "w3" else (marlin.mul_2_4_meta3 if wl == "meta3" else marlin.mul_2_4)
+        meta_key = "meta3" if wl == "meta3" else "meta"
+        for M in Ms:
+            for name, K, N in shapes:
+                A = synth.make_activation(M, K, synth.SEED_BASE + M, device=device)
+                calls.append(Call(name, K, N, M, weights[name], A, fn, meta_key))
+        cfg = {"workload": {"decode": "decode_sweep_llama2_7b", "meta3": "decode_sweep_llama2_7b_meta3",
+                            "w3": "w3_values_llama2_7b"}[wl],
+               "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in shapes], "groupsize": 128,
+               "weight_copies": copies,
+               "rotated_weight_bytes": {n: copies[n] * synth.weight_bytes(K, N, bits, 128) for n, K, N in shapes}}
+    elif wl == "prefill":
+        Ms = args.prefill_m
+        for i, (name, K, N) in enumerate(LLAMA70B):
+            w = make_copies(K, N, synth.SEED_BASE + 11 + i, 4, 1, device)
+            for M in Ms:
+                A = synth.make_activation(M, K, synth.SEED_BASE + M, device=device)
+                calls.append(Call(name, K, N, M, w, A, marlin.mul_2_4))
+        cfg = {"workload": "prefill_sweep_llama2_70b", "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in LLAMA70B],
+               "groupsize": 128}
+    elif wl == "stack":
+        Ms = [1, 8, 32]
+        layers = []
+        for l in range(32):
+            layers.append({name: make_copies(K, N, synth.SEED_BASE + 1000 + 4 * l + i, 4, 1, device)
+                           for i, (name, K, N) in enumerate(LLAMA7B)})
+        for M in Ms:
+            As = {K: synth.make_activation(M, K, synth.SEED_BASE + M, device=device) for _, K, _ in LLAMA7B}
+            for l in range(32):
+                for name, K, N in LLAMA7B:
+                    calls.append(Call(f"L{l}.{name}", K, N, M, layers[l][name], As[K], marlin.mul_2_4))
+        cfg = {"workload": "decode_stack_32x_llama2_7b", "M": Ms, "layers": 32, "groupsize": 128}
+    else:
+        raise SystemExit(f"unknown workload {wl}")
+    return calls, cfg
+
+
+def main():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="decode", choices=["decode", "prefill", "w3", "meta3", "stack"])
+    p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-per-call", action="store_true")
+    args = p.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        raise SystemExit("bench.py measures one GPU: the 2:4 GEMM has no multi-GPU path in this build "
+                         "(column sharding needs no communication; see DESIGN.md). Run with --gpus 1.")
+    if not torch.cuda.is_available():
+        raise SystemExit("no GPU visible")
+    _lib.load()
+    device = "cuda:0"
+    log(f"bench: workload={args.workload} steps={args.steps} warmup={args.warmup}")
+    calls, cfg = build_workload(args, device)
+    log(f"bench: {len(calls)} calls per step built")
+    g = graph_of(calls)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        g.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    launches = args.steps * len(calls)
+    step_bytes = sum(c.wbytes for c in calls)
+    step_flops = sum(c.flops for c in calls)
+    ms_per_step = wall * 1e3 / args.steps
+    log(f"bench: timed {args.steps} steps: wall {wall * 1e3:.3f} ms, gpu {gpu_ms:.3f} ms")
+    gbps = step_bytes * args.steps / (gpu_ms * 1e6)
+    tflops = step_flops * args.steps / (gpu_ms * 1e9)
+    avg_launch_us = gpu_ms * 1e3 / launches
+    if args.workload == "prefill":
+        value, unit = tflops, "TFLOP/s"
+        roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": SPARSE_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / SPARSE_F16_PEAK_TFLOPS, 4), "traffic": None}
+    else:
+        value, unit = gbps, "GB/s"
+        roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": None}
+    roof["kernel"] = "sm24::sm24_gemm_kernel"
+    roof["avg_launch_us"] = round(avg_launch_us, 3)
+    roof["algorithmic_bytes_per_step"] = step_bytes
+    out = {"metric": METRIC, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f16", "data": "synthetic", "config": cfg, "roofline": roof}
+    if not args.no_per_call:
+        log("bench: per-call timing")
+        pcs = per_call_stats(calls if args.workload != "stack" else calls[:4])
+        out["per_call"] = pcs
+    if not args.no_cpu_baseline and args.workload in ("decode", "meta3", "w3", "stack"):
+        log("bench: cpu baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline()
+    elif not args.no_cpu_baseline:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

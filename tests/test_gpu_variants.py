@@ -71,11 +71,13 @@ def test_w3_gemm_config4(M, K, N):
 
 
 def test_w3_gemm_small_full_oracle():
-    for M, N, K, g in ((5, 512, 1024, -1), (16, 768, 192, -1), (33, 1024, 2048, 128)):
+    # (K=192 needs the reference's 64-deep tile: the automatic 128-deep tile rejects it)
+    for M, N, K, g, tk, tm in ((5, 512, 1024, -1, -1, -1), (16, 768, 192, -1, 64, 256),
+                               (33, 1024, 2048, 128, -1, -1)):
         wt = synth.make_weight(K, N, M, g, bits=3, device=DEV)
         A = synth.make_activation(M, K, M, device=DEV)
         C = torch.empty(M, N, dtype=torch.half, device=DEV)
-        marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C, wt["s"], _ws(N))
+        marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C, wt["s"], _ws(N), tk, tm)
         torch.cuda.synchronize()
         assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), f"w3 {M}x{N}x{K}")
 
