@@ -85,6 +85,34 @@ __device__ __forceinline__ uint32_t idx_pair(uint32_t d0, uint32_t d1, uint32_t 
   return x | (y << 4);
 }
 
+enum : int { VAL4 = 0, VAL3 = 1 };
+enum : int { META4 = 0, META3 = 1 };
+
+// 4-bit nibble tables of the 3-bit metadata decoders (pair.cu:11 of the
+// reference's decoder_dependency experiment): code c -> nibble (LUT >> 4c) & 15.
+constexpr uint32_t lut_of(const int (&t)[8]) {
+  uint32_t v = 0;
+  for (int i = 0; i < 8; i++) v |= (uint32_t)t[i] << (4 * i);
+  return v;
+}
+constexpr int kDecHigh[8] = {14, 13, 8, 13, 3, 4, 9, 12};
+constexpr int kDecLow[8] = {12, 13, 14, 10, 8, 9, 4, 0};
+constexpr uint32_t kLutHigh = lut_of(kDecHigh);
+constexpr uint32_t kLutLow = lut_of(kDecLow);
+
+struct GemmArgs {
+  const _Float16* A;
+  const void* B;
+  const void* meta;
+  const _Float16* s;
+  _Float16* C;
+  const _Float16* zeros;  // >= 64 zero bytes (activation rows that do not exist)
+  int M, N, K;
+  int splits;
+  float* partial;  // [splits][M][N] when splits > 1
+  uint32_t* counters;  // [gridDim.z][gridDim.x] arrival counters, zero between launches
+};
+
 template <int ABID>
 __device__ __forceinline__ float4_t smfmac32(half4_t a, half8_t b, float4_t c, uint32_t idx) {
   return __builtin_amdgcn_smfmac_f32_16x16x32_f16(a, b, c, (int)idx, 0, ABID);

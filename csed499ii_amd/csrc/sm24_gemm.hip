@@ -20,6 +20,7 @@
 // (Marlin_2_4 at 42-723, host dispatch marlin_cuda_2_4 at 751-830).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <map>
@@ -29,50 +30,27 @@
 #include <vector>
 
 #include "sm24_device.h"
+#include "sm24_decode.h"
 #include "../../include/marlin_hip.h"
 
 namespace sm24 {
 
-enum : int { VAL4 = 0, VAL3 = 1 };
-enum : int { META4 = 0, META3 = 1 };
-
-struct GemmArgs {
-  const _Float16* A;
-  const void* B;
-  const void* meta;
-  const _Float16* s;
-  _Float16* C;
-  int M, N, K;
-  int splits;
-  float* partial;  // [splits][M][N] when splits > 1
-  uint32_t* counters;  // [gridDim.z][gridDim.x] tagged arrival counters
-  uint32_t tag;        // launch tag, 1..2^24-1
-};
-
-// 4-bit nibble tables of the 3-bit metadata decoders (pair.cu:11 of the
-// reference's decoder_dependency experiment): code c -> nibble (LUT >> 4c) & 15.
-constexpr uint32_t lut_of(const int (&t)[8]) {
-  uint32_t v = 0;
-  for (int i = 0; i < 8; i++) v |= (uint32_t)t[i] << (4 * i);
-  return v;
-}
-constexpr int kDecHigh[8] = {14, 13, 8, 13, 3, 4, 9, 12};
-constexpr int kDecLow[8] = {12, 13, 14, 10, 8, 9, 4, 0};
-constexpr uint32_t kLutHigh = lut_of(kDecHigh);
-constexpr uint32_t kLutLow = lut_of(kDecLow);
-
-template <int BB>
+// Raw operands of one k-block for one lane, as loaded (decoding happens at use, so
+// that a deep ring of these stays in flight).
+template <int BB, int VF, int MF>
 struct Frag {
-  uint32_t w0, w1;   // packed words j = 2*jb, 2*jb+1 (nibble form)
-  uint32_t idx;      // sparse-index bytes, byte (jj + 2*blk)
-  half4_t sc;        // grouped scales {s(jj0,b0), s(jj0,b1), s(jj1,b0), s(jj1,b1)}
-  half8_t act[BB];   // activation B operands
+  u32x2 w;              // packed words j = 2*jb, 2*jb+1 (VAL3: the 8 bytes holding them)
+  u32x4 m0;             // META4: units 16jb+2g, +1; META3: code words X
+  u32x4 m1;             // META3 only: code words Y
+  half4_t sc;           // grouped scales {s(jj0,b0), s(jj0,b1), s(jj1,b0), s(jj1,b1)}
+  half8_t act[BB];      // activation B operands
 };
 
-template <int BB, bool GROUPED, int VF, int MF>
-__global__ __launch_bounds__(256) void sm24_gemm_kernel(GemmArgs a) {
+template <int BB, int NW, bool GROUPED, int VF, int MF>
+__global__ __launch_bounds__(64 * NW) void sm24_gemm_kernel(GemmArgs a) {
+  constexpr int NT = 64 * NW;  // threads per workgroup
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
   const int chunk = blockIdx.x;
   const int split = blockIdx.y;
   const int bt = blockIdx.z;
@@ -96,56 +74,33 @@ __global__ __launch_bounds__(256) void sm24_gemm_kernel(GemmArgs a) {
   const _Float16* sp = a.s + 64 * chunk + 8 * g + 4 * jb;
   const int row0 = 16 * BB * bt + rho;
 
-  auto fetch = [&](int r, Frag<BB>& f) {
+  auto fetch = [&](int r, bool live, Frag<BB, VF, MF>& f) {
     if constexpr (VF == VAL4) {
-      const u32x2 w = *reinterpret_cast<const u32x2*>(bw + (size_t)r * (2 * (size_t)N));
-      f.w0 = w.x;
-      f.w1 = w.y;
+      f.w = *reinterpret_cast<const u32x2*>(bw + (size_t)r * (2 * (size_t)N));
     } else {
-      const u32x2 w = *reinterpret_cast<const u32x2_a4*>(b3 + (size_t)r * (6 * (size_t)N));
-      const uint64_t v = ((uint64_t)w.y << 32 | w.x) >> (16 * jb);
-      f.w0 = spread3((uint32_t)v & 0xFFFFFFu);
-      f.w1 = spread3((uint32_t)(v >> 24) & 0xFFFFFFu);
+      f.w = *reinterpret_cast<const u32x2_a4*>(b3 + (size_t)r * (6 * (size_t)N));
     }
     if constexpr (MF == META4) {
-      const u32x4 md = *reinterpret_cast<const u32x4*>(mw + (size_t)r * N);
-      f.idx = idx_pair(md.x, md.y, sh) | (idx_pair(md.z, md.w, sh) << 8);
+      f.m0 = *reinterpret_cast<const u32x4*>(mw + (size_t)r * N);
     } else {
-      // 48-word group for (k-block r, chunk): words 0..15 / 16..31 / 32..47 hold
-      // the 48-bit "first" and "second" code pairs of the 64 metadata words.
       const uint32_t* base = m3 + (size_t)r * (size_t)(3 * N / 4);
-      const u32x4 X = *reinterpret_cast<const u32x4*>(base);
-      const u32x4 Y = *reinterpret_cast<const u32x4*>(base + 16);
-      const uint32_t lut = jb ? kLutLow : kLutHigh;
-      uint32_t xs[4];
-#pragma unroll
-      for (int v = 0; v < 4; v++) {
-        uint32_t c24;
-        if ((g >> 2) == 0) {
-          c24 = jb ? ((X[v] >> 24) | ((Y[v] & 0xFFFFu) << 8)) : (X[v] & 0xFFFFFFu);
-        } else {
-          c24 = jb ? ((Y[v] >> 8) & 0xFFFFFFu) : (((X[v] >> 16) | (Y[v] << 16)) & 0xFFFFFFu);
-        }
-        const uint32_t ca = (c24 >> (3 * h)) & 7u;
-        const uint32_t cb = (c24 >> (3 * h + 12)) & 7u;
-        xs[v] = ((lut >> (4 * ca)) & 15u) | (((lut >> (4 * cb)) & 15u) << 16);
-      }
-      f.idx = (xs[0] | (xs[1] << 4)) | ((xs[2] | (xs[3] << 4)) << 8);
+      f.m0 = *reinterpret_cast<const u32x4*>(base);
+      f.m1 = *reinterpret_cast<const u32x4*>(base + 16);
     }
     if constexpr (GROUPED) {
       f.sc = *reinterpret_cast<const half4_t*>(sp + (size_t)(r >> 2) * N);
     }
 #pragma unroll
     for (int bb = 0; bb < BB; bb++) {
+      // Rows past M (and slots past the range, live == false) read zeros from a
+      // small zero-filled buffer: the load is unconditional, only its address is
+      // selected, so the ring keeps a fixed shape.
       const int m = row0 + 16 * bb;
-      if (m < M) {
-        const _Float16* ap = a.A + (size_t)m * K + 32 * r + 4 * h;
-        const half4_t lo = *reinterpret_cast<const half4_t*>(ap);
-        const half4_t hi = *reinterpret_cast<const half4_t*>(ap + 16);
-        f.act[bb] = (half8_t){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-      } else {
-        f.act[bb] = (half8_t){};
-      }
+      const _Float16* ap =
+          (live && m < M) ? a.A + (size_t)m * K + 32 * r + 4 * h : a.zeros;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(ap);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(ap + 16);
+      f.act[bb] = __builtin_bit_cast(half8_t, (u32x4){lo.x, lo.y, hi.x, hi.y});
     }
   };
 
@@ -155,18 +110,49 @@ __global__ __launch_bounds__(256) void sm24_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int t = 0; t < 4; t++) acc[bb][t] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const Frag<BB>& f) {
+  auto compute = [&](const Frag<BB, VF, MF>& f) {
+    uint32_t w0, w1, idx;
+    if constexpr (VF == VAL4) {
+      w0 = f.w.x;
+      w1 = f.w.y;
+    } else {
+      const uint64_t v = ((uint64_t)f.w.y << 32 | f.w.x) >> (16 * jb);
+      w0 = spread3((uint32_t)v & 0xFFFFFFu);
+      w1 = spread3((uint32_t)(v >> 24) & 0xFFFFFFu);
+    }
+    if constexpr (MF == META4) {
+      idx = idx_pair(f.m0.x, f.m0.y, sh) | (idx_pair(f.m0.z, f.m0.w, sh) << 8);
+    } else {
+      // 48-word group for (k-block, chunk): words 0..15 / 16..31 / 32..47 hold the
+      // 48-bit "first" and "second" code pairs of the 64 metadata words.
+      const uint32_t lut = jb ? kLutLow : kLutHigh;
+      uint32_t xs[4];
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const uint32_t X = f.m0[v], Y = f.m1[v];
+        uint32_t c24;
+        if ((g >> 2) == 0) {
+          c24 = jb ? ((X >> 24) | ((Y & 0xFFFFu) << 8)) : (X & 0xFFFFFFu);
+        } else {
+          c24 = jb ? ((Y >> 8) & 0xFFFFFFu) : (((X >> 16) | (Y << 16)) & 0xFFFFFFu);
+        }
+        const uint32_t ca = (c24 >> (3 * h)) & 7u;
+        const uint32_t cb = (c24 >> (3 * h + 12)) & 7u;
+        xs[v] = ((lut >> (4 * ca)) & 15u) | (((lut >> (4 * cb)) & 15u) << 16);
+      }
+      idx = (xs[0] | (xs[1] << 4)) | ((xs[2] | (xs[3] << 4)) << 8);
+    }
     half4_t a00, a01, a10, a11;  // (jj, blk)
     if constexpr (VF == VAL4) {
-      a00 = dequant4(f.w0);
-      a01 = dequant4(f.w0 >> 8);
-      a10 = dequant4(f.w1);
-      a11 = dequant4(f.w1 >> 8);
+      a00 = dequant4(w0);
+      a01 = dequant4(w0 >> 8);
+      a10 = dequant4(w1);
+      a11 = dequant4(w1 >> 8);
     } else {
-      a00 = dequant3(f.w0);
-      a01 = dequant3(f.w0 >> 8);
-      a10 = dequant3(f.w1);
-      a11 = dequant3(f.w1 >> 8);
+      a00 = dequant3(w0);
+      a01 = dequant3(w0 >> 8);
+      a10 = dequant3(w1);
+      a11 = dequant3(w1 >> 8);
     }
     if constexpr (GROUPED) {
       a00 = scale4(a00, f.sc.x);
@@ -176,32 +162,47 @@ __global__ __launch_bounds__(256) void sm24_gemm_kernel(GemmArgs a) {
     }
 #pragma unroll
     for (int bb = 0; bb < BB; bb++) {
-      acc[bb][0] = smfmac32<0>(a00, f.act[bb], acc[bb][0], f.idx);
-      acc[bb][1] = smfmac32<1>(a10, f.act[bb], acc[bb][1], f.idx);
-      acc[bb][2] = smfmac32<2>(a01, f.act[bb], acc[bb][2], f.idx);
-      acc[bb][3] = smfmac32<3>(a11, f.act[bb], acc[bb][3], f.idx);
+      acc[bb][0] = smfmac32<0>(a00, f.act[bb], acc[bb][0], idx);
+      acc[bb][1] = smfmac32<1>(a10, f.act[bb], acc[bb][1], idx);
+      acc[bb][2] = smfmac32<2>(a01, f.act[bb], acc[bb][2], idx);
+      acc[bb][3] = smfmac32<3>(a11, f.act[bb], acc[bb][3], idx);
     }
   };
 
-  int r = kb0 + wave;
-  if (r < kb1) {
-    Frag<BB> cur;
-    fetch(r, cur);
-    while (true) {
-      const int rn = r + 4;
-      Frag<BB> nxt;
-      const bool more = rn < kb1;
-      if (more) fetch(rn, nxt);
-      compute(cur);
-      if (!more) break;
-      cur = nxt;
-      r = rn;
+  // Each wave streams a contiguous quarter of the split's k-blocks through a ring of
+  // U in-flight fragments: the load of k-block r+U is issued as soon as k-block r
+  // has been consumed, so U k-blocks per wave are always on their way from HBM.
+  // Slots past the end re-read the last k-block (a cache hit) with zero activations.
+  constexpr int U = BB == 1 ? 8 : (BB == 2 ? 6 : 4);
+  const int span = kb1 - kb0;
+  const int r0 = kb0 + (int)(((long long)span * wave) / NW);
+  const int r1 = kb0 + (int)(((long long)span * (wave + 1)) / NW);
+  if (r1 > r0) {
+    const int rlast = r1 - 1;
+    Frag<BB, VF, MF> ring[U];
+#pragma unroll
+    for (int i = 0; i < U; i++) {  // prologue, issued in slot order
+      fetch(r0 + i < r1 ? r0 + i : rlast, r0 + i < r1, ring[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int base = r0; base < r1; base += U) {
+#pragma unroll
+      for (int i = 0; i < U; i++) {
+        // Scheduling barriers keep the decode of a fragment at its use: left free, the
+        // scheduler pulls it up next to the load issued one ring-turn earlier and
+        // the wave stalls on that load.
+        compute(ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        const int rn = base + i + U;
+        fetch(rn < r1 ? rn : rlast, rn < r1, ring[i]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
-  // ---- reduce the four waves in LDS: red[wave][row][col], col = n within chunk ----
+  // ---- reduce the NW waves in LDS: red[wave][row][col], col = n within chunk ----
   constexpr int RS = 65;  // padded row stride (floats)
-  __shared__ float red[4][16 * BB][RS];
+  __shared__ float red[NW][16 * BB][RS];
 #pragma unroll
   for (int bb = 0; bb < BB; bb++) {
 #pragma unroll
@@ -220,11 +221,13 @@ __global__ __launch_bounds__(256) void sm24_gemm_kernel(GemmArgs a) {
   const int ntile = 16 * BB * 64;
   const int ncol0 = 64 * chunk;
   if (a.splits == 1) {
-    for (int e = threadIdx.x; e < ntile; e += 256) {
+    for (int e = threadIdx.x; e < ntile; e += NT) {
       const int ml = e >> 6, nl = e & 63;
       const int m = 16 * BB * bt + ml;
       if (m >= M) continue;
-      const float v = red[0][ml][nl] + red[1][ml][nl] + red[2][ml][nl] + red[3][ml][nl];
+      float v = red[0][ml][nl];
+#pragma unroll
+      for (int w = 1; w < NW; w++) v += red[w][ml][nl];
       _Float16 o = (_Float16)v;
       if constexpr (!GROUPED) o = o * a.s[ncol0 + nl];
       a.C[(size_t)m * N + ncol0 + nl] = o;
@@ -232,43 +235,52 @@ __global__ __launch_bounds__(256) void sm24_gemm_kernel(GemmArgs a) {
     return;
   }
 
-  for (int e = threadIdx.x; e < ntile; e += 256) {
+  // Split-K hand-off.  The scratch lives in uncached device memory and every access
+  // to it is a device-scope atomic, so partials and counters meet at the
+  // device-coherent point without any L2-wide write-back or invalidate (which an
+  // agent-scope fence would issue on every XCD).  Ordering: each thread waits for
+  // its own partial stores to complete before the workgroup barrier; the counter is
+  // bumped only after that barrier.
+  for (int e = threadIdx.x; e < ntile; e += NT) {
     const int ml = e >> 6, nl = e & 63;
     const int m = 16 * BB * bt + ml;
     if (m >= M) continue;
-    const float v = red[0][ml][nl] + red[1][ml][nl] + red[2][ml][nl] + red[3][ml][nl];
+    float v = red[0][ml][nl];
+#pragma unroll
+    for (int w = 1; w < NW; w++) v += red[w][ml][nl];
     __hip_atomic_store(a.partial + ((size_t)split * M + m) * N + ncol0 + nl, v, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
-  // Arrival counter of this (chunk, batch tile): bits 31..8 carry the launch's tag,
-  // bits 7..0 the number of splits that have arrived.  A slot holding another tag
-  // (a finished launch resets it to 0; anything else is stale) restarts at 1.
+  // Arrival counter of this (chunk, batch tile); the last of the splits to arrive
+  // reduces and resets it.  A single fetch-add per workgroup: no retry loop.
   __shared__ uint32_t arrived;
   uint32_t* cnt = a.counters + bt * gridDim.x + chunk;
-  if (threadIdx.x == 0) {
-    uint32_t old = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t nv;
-    while (true) {
-      nv = ((old >> 8) == a.tag) ? old + 1u : ((a.tag << 8) | 1u);
-      if (__hip_atomic_compare_exchange_strong(cnt, &old, nv, __ATOMIC_ACQ_REL, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT))
-        break;
-    }
-    arrived = nv & 0xFFu;
-  }
+  if (threadIdx.x == 0) arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   __syncthreads();
   if (arrived != (uint32_t)a.splits) return;
-  __threadfence();
-  for (int e = threadIdx.x; e < ntile; e += 256) {
+  for (int e = threadIdx.x; e < ntile; e += NT) {
     const int ml = e >> 6, nl = e & 63;
     const int m = 16 * BB * bt + ml;
     if (m >= M) continue;
+    const float* pp = a.partial + (size_t)m * N + ncol0 + nl;
+    const size_t pstride = (size_t)M * N;
     float v = 0.f;
-    for (int q = 0; q < a.splits; q++)
-      v += __hip_atomic_load(a.partial + ((size_t)q * M + m) * N + ncol0 + nl, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    int q = 0;
+    for (; q + 4 <= a.splits; q += 4) {  // four loads in flight, summed in split order
+      const float p0 = __hip_atomic_load(pp + (q + 0) * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float p1 = __hip_atomic_load(pp + (q + 1) * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float p2 = __hip_atomic_load(pp + (q + 2) * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float p3 = __hip_atomic_load(pp + (q + 3) * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v += p0;
+      v += p1;
+      v += p2;
+      v += p3;
+    }
+    for (; q < a.splits; q++) v += __hip_atomic_load(pp + q * pstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     _Float16 o = (_Float16)v;
     if constexpr (!GROUPED) o = o * a.s[ncol0 + nl];
     a.C[(size_t)m * N + ncol0 + nl] = o;
@@ -294,12 +306,29 @@ struct Scratch {
 // Buffers are never freed: a captured graph may still refer to an old one.
 std::mutex g_scratch_mu;
 std::map<int, Scratch> g_scratch;
-std::map<int, uint32_t> g_tag;
+std::map<int, void*> g_zeros;
+
+constexpr size_t kZeroBytes = 256;
+
+// A small zero-filled buffer per device (read by lanes that have no activation row).
+int get_zeros(int dev, const _Float16** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  void*& z = g_zeros[dev];
+  if (!z) {
+    void* p = nullptr;
+    if (hipMalloc(&p, kZeroBytes) != hipSuccess || hipMemset(p, 0, kZeroBytes) != hipSuccess) {
+      set_error("marlin_hip: allocation of the zero buffer failed");
+      return MARLIN_HIP_ERR_LAUNCH;
+    }
+    z = p;
+  }
+  *out = static_cast<const _Float16*>(z);
+  return MARLIN_HIP_OK;
+}
 
 constexpr size_t kCounterBytes = 64 * 1024;  // up to 16384 (chunk, batch-tile) counters
 
-int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** counters, float** partial,
-                uint32_t* tag) {
+int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** counters, float** partial) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   Scratch& s = g_scratch[dev];
   const size_t need = kCounterBytes + partial_bytes;
@@ -312,9 +341,12 @@ int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** co
     }
     size_t nb = need > 2 * s.bytes ? need : 2 * s.bytes;
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, nb);
+    // Uncached: split-K partials and counters are exchanged between workgroups that
+    // run on different XCDs, whose L2 caches are not coherent with each other.
+    // Never freed (see above), as uncached memory must not be recycled once read.
+    hipError_t e = hipExtMallocWithFlags(&p, nb, hipDeviceMallocUncached);
     if (e != hipSuccess) {
-      set_error(std::string("marlin_hip: hipMalloc of scratch failed: ") + hipGetErrorString(e));
+      set_error(std::string("marlin_hip: uncached allocation of scratch failed: ") + hipGetErrorString(e));
       return MARLIN_HIP_ERR_LAUNCH;
     }
     e = hipMemset(p, 0, kCounterBytes);
@@ -325,9 +357,6 @@ int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** co
     s.ptr = p;
     s.bytes = nb;
   }
-  uint32_t& t = g_tag[dev];
-  t = (t % 0xFFFFFFu) + 1u;  // 1 .. 2^24-1; 0 marks a free counter
-  *tag = t;
   *counters = static_cast<uint32_t*>(s.ptr);
   *partial = reinterpret_cast<float*>(static_cast<char*>(s.ptr) + kCounterBytes);
   return MARLIN_HIP_OK;
@@ -339,6 +368,17 @@ struct Plan {
   int ztiles;
 };
 
+// Workgroups per compute unit the planner aims for (MARLIN_HIP_WGS_PER_CU overrides;
+// read once).
+int wgs_per_cu() {
+  static const int v = [] {
+    const char* e = getenv("MARLIN_HIP_WGS_PER_CU");
+    int x = e ? atoi(e) : 0;
+    return x > 0 && x <= 64 ? x : 2;
+  }();
+  return v;
+}
+
 Plan plan_for(int M, int N, int K, int cus) {
   Plan p;
   p.bb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
@@ -346,11 +386,11 @@ Plan plan_for(int M, int N, int K, int cus) {
   const int chunks = N / 64;
   const int nkb = K / 32;
   const long long tiles = (long long)chunks * p.ztiles;
-  const long long target = 2LL * cus;
+  const long long target = (long long)wgs_per_cu() * cus;
   int splits = (int)((target + tiles - 1) / tiles);
-  const int max_splits = nkb / 4 > 0 ? nkb / 4 : 1;  // at least one k-block per wave
+  const int max_splits = nkb / 8 > 0 ? nkb / 8 : 1;  // at least two k-blocks per wave
   if (splits > max_splits) splits = max_splits;
-  if (splits > 32) splits = 32;
+  if (splits > 64) splits = 64;
   if (splits < 1) splits = 1;
   p.splits = splits;
   return p;
@@ -358,7 +398,8 @@ Plan plan_for(int M, int N, int K, int cus) {
 
 template <int BB, bool GROUPED, int VF, int MF>
 hipError_t launch_t(const GemmArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((sm24_gemm_kernel<BB, GROUPED, VF, MF>), grid, dim3(256), 0, stream, a);
+  constexpr int NW = BB == 1 ? 8 : 4;  // waves per workgroup (LDS reduction buffer < 64 KiB)
+  hipLaunchKernelGGL((sm24_gemm_kernel<BB, NW, GROUPED, VF, MF>), grid, dim3(64 * NW), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -372,6 +413,52 @@ hipError_t launch_v(const GemmArgs& a, int bb, bool grouped, dim3 grid, hipStrea
   if (bb == 1) return launch_t<1, false, VF, MF>(a, grid, stream);
   if (bb == 2) return launch_t<2, false, VF, MF>(a, grid, stream);
   return launch_t<4, false, VF, MF>(a, grid, stream);
+}
+
+// Column-tile width of the decode kernel: the widest tile (fewest re-reads of the
+// activations) that still gives every compute unit at least one workgroup.
+int decode_tile_cols(int N, int cus) {
+  if (N / 64 >= cus) return 64;
+  if (N / 32 >= cus) return 32;
+  return 16;
+}
+
+// Waves per decode workgroup (MARLIN_HIP_DECODE_WAVES overrides; read once).
+int decode_waves() {
+  static const int v = [] {
+    const char* e = getenv("MARLIN_HIP_DECODE_WAVES");
+    const int x = e ? atoi(e) : 0;
+    return (x == 4 || x == 8 || x == 16) ? x : 8;
+  }();
+  return v;
+}
+
+template <int TC, int NW, bool GROUPED>
+void launch_decode_nw(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
+  const dim3 grid(a.N / TC), block(64 * NW);
+  if (vf == VAL3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, GROUPED, VAL3, META4>), grid, block, 0, stream, a);
+  else if (mf == META3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, GROUPED, VAL4, META3>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, GROUPED, VAL4, META4>), grid, block, 0, stream, a);
+}
+
+template <int TC, bool GROUPED>
+hipError_t launch_decode_t(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
+  const int nw = decode_waves();
+  if (nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, vf, mf, stream);
+  else if (nw == 16) launch_decode_nw<TC, 16, GROUPED>(a, vf, mf, stream);
+  else launch_decode_nw<TC, 8, GROUPED>(a, vf, mf, stream);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode(const GemmArgs& a, int tc, int vf, int mf, bool grouped, hipStream_t stream) {
+  if (grouped) {
+    if (tc == 64) return launch_decode_t<64, true>(a, vf, mf, stream);
+    if (tc == 32) return launch_decode_t<32, true>(a, vf, mf, stream);
+    return launch_decode_t<16, true>(a, vf, mf, stream);
+  }
+  if (tc == 64) return launch_decode_t<64, false>(a, vf, mf, stream);
+  if (tc == 32) return launch_decode_t<32, false>(a, vf, mf, stream);
+  return launch_decode_t<16, false>(a, vf, mf, stream);
 }
 
 // Shape/tile validation with the reference's rules and error codes
@@ -423,6 +510,32 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       sms = 256;
   }
   const int M = prob_n, N = prob_m, K = prob_k;
+  if (M <= 16) {
+    // Decode: one workgroup per column tile over the whole K (no split-K).
+    GemmArgs d{};
+    d.A = static_cast<const _Float16*>(A);
+    d.B = B;
+    d.meta = meta;
+    d.s = static_cast<const _Float16*>(s);
+    d.C = static_cast<_Float16*>(C);
+    d.M = M;
+    d.N = N;
+    d.K = K;
+    d.splits = 1;
+    err = get_zeros(dev, &d.zeros);
+    if (err != MARLIN_HIP_OK) {
+      if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+      return err;
+    }
+    const int tc = decode_tile_cols(N, sms);
+    hipError_t e = launch_decode(d, tc, vf, mf, groupsize != -1, stream);
+    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+    if (e != hipSuccess) {
+      set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
+      return MARLIN_HIP_ERR_LAUNCH;
+    }
+    return MARLIN_HIP_OK;
+  }
   Plan plan = plan_for(M, N, K, sms);
   GemmArgs a;
   a.A = static_cast<const _Float16*>(A);
@@ -436,15 +549,18 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
   a.splits = plan.splits;
   a.partial = nullptr;
   a.counters = nullptr;
-  a.tag = 0;
+  err = get_zeros(dev, &a.zeros);
+  if (err != MARLIN_HIP_OK) {
+    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+    return err;
+  }
   const int chunks = N / 64;
   if (plan.splits > 1) {
     if ((size_t)chunks * plan.ztiles * sizeof(int) > kCounterBytes) {
       plan.splits = 1;
       a.splits = 1;
     } else {
-      err = get_scratch(dev, stream, (size_t)plan.splits * M * N * sizeof(float), &a.counters, &a.partial,
-                        &a.tag);
+      err = get_scratch(dev, stream, (size_t)plan.splits * M * N * sizeof(float), &a.counters, &a.partial);
       if (err != MARLIN_HIP_OK) {
         if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
         return err;
