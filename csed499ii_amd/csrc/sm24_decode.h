@@ -1,56 +1,74 @@
 // Decode-sized (M <= 16) 2:4 INT4 x FP16 GEMM for gfx950, no split-K.
 //
-// One workgroup owns a tile of TC output columns (TC = 16, 32 or 64, chosen so that
-// the tiles cover the compute units) over the whole K, so the result never crosses
-// workgroups: a cross-workgroup hand-off costs microseconds on this multi-XCD part,
-// more than the whole weight stream of a 4096x4096 layer.
+// One workgroup owns a tile of TC output columns (TC = 16, 32 or 64) over the whole
+// K, so the result never crosses workgroups: a cross-workgroup hand-off costs
+// microseconds on this multi-XCD part, more than the whole weight stream of a
+// 4096x4096 layer.
 //
-// The tile's packed weight is streamed in stages of KS k-blocks (KS * TC = 64 * NW
-// column-k-blocks, 800 bytes of values + metadata + scales per wave).  Every thread owns one
-// 16-byte piece of each stage (thread t: the t-th piece, same slot in every stage);
-// a register ring keeps D stages in flight, i.e. D * 0.8 KiB per wave.  When a
-// stage's pieces arrive they are written to one of two LDS buffers and, after a
-// barrier, the four waves read their MFMA operands from LDS in the v_smfmac lane
-// order (the 16-byte pieces are coalesced in HBM but hold 8 columns x 4 k-rows,
-// while an MFMA row needs one column).
+// Cost model (measured on MI355X): every 16-byte vector load instruction occupies a
+// compute unit's address path for ~16 cycles whatever its lanes do (full, masked,
+// duplicated or out of range alike), so the kernel issues as few load instructions
+// as the bytes allow and fills every lane with a distinct useful 16-byte piece.
 //
-// Wave w computes k-blocks [w*KS/NW, (w+1)*KS/NW) of every stage for all 16-column
-// blocks of the tile; activations (the dense B operand) come from L2, prefetched
-// two or three stages ahead.  The four waves' accumulators are reduced in LDS.
+// A stage covers KS k-blocks of the tile (KS * TC = 64 * NW column-k-blocks).  Its
+// pieces - packed values, metadata, scales and, for MB < 16, the activation rows -
+// form one list of P 16-byte pieces; thread t loads pieces t, t + NT, ... (SL slots)
+// of every stage, rows clamped to the operand, into a register ring D stages deep.
+// When a stage is due its pieces are written to one of two LDS buffers and, after
+// one barrier, the NW waves read their MFMA operands from LDS.  For MB = 16 every
+// lane of the activation operand is a real batch row, so each wave loads its own
+// operands straight into the ring instead.  Batch rows past M read row M-1 (their
+// outputs are not stored); k-blocks past K read zero activations, so the last stage
+// needs no per-k-block branch.
+//
+// MFMA (v_smfmac_f32_16x16x32_f16) lane roles: lane (rho, h) = (l % 16, l / 16)
+// holds output column n0 + 16*cb + rho, dense groups 2h and 2h+1 of a k-block; its
+// activation operand is batch row rho, dense K 8h .. 8h+7 (16 contiguous bytes).
+// Group d of a column sits in word t = d mod 4 of the packed row, nibble pair
+// 2*blk + (d >= 4): lane group h reads words t0 = 2*(h&1), t0+1.  Wave w computes
+// k-blocks [w*KPW, (w+1)*KPW) of every stage for all column blocks; the waves'
+// partial sums are reduced in LDS at the end.
 #pragma once
 #include "sm24_device.h"
 
 namespace sm24 {
 
-template <int TC, int NW, bool GROUPED, int VF, int MF>
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+
+template <int TC, int NW, int MB, bool GROUPED, int VF, int MF>
 __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int NT = 64 * NW;                           // threads
   constexpr int NCB = TC / 16;                          // 16-column MFMA blocks per tile
   constexpr int KPW = 64 / TC;                          // k-blocks per wave per stage
-  constexpr int KS = KPW * NW;                          // k-blocks per stage (64*NW column-k-blocks)
+  constexpr int KS = KPW * NW;                          // k-blocks per stage
   constexpr int BPK = VF == VAL4 ? TC / 2 : 3 * TC / 8;  // 16-byte value pieces per k-block
   // 16-byte metadata pieces per k-block: the tile's 4*TC bytes of 4-bit metadata, or
   // of the 3-bit code words (the whole 192-byte group when TC == 64).
   constexpr int MPK = (MF == META3 && TC == 64) ? 12 : TC / 4;
   constexpr int SPG = TC / 8;                           // 16-byte scale pieces per scale group
+  constexpr bool STAGED = MB < 16;                      // activations through LDS
   constexpr int NB = KS * BPK;
   constexpr int NM = KS * MPK;
   constexpr int NSC = GROUPED ? (KS / 4) * SPG : 0;
-  constexpr int NP = NB + NM + NSC;                     // pieces per stage (about 50 per wave)
-  constexpr int BBYTES = NB * 16, MBYTES = NM * 16, SBYTES = NSC * 16;
-  constexpr int DUMMY = BBYTES + MBYTES + SBYTES;       // threads without a piece write here
-  constexpr int STAGE = DUMMY + (NT - NP) * 16;
-  // Stages in flight D and activation ring ARS (prefetch distance ARS-1), sized so
-  // that a wave never has more than 63 loads outstanding (the vmcnt limit):
-  // D * (1 + KPW) <= 63.
-  // With 16 waves (4 per SIMD) the register budget is 128: shallower rings.
-  constexpr int D = NW == 16 ? (TC == 64 ? 12 : 8) : (TC == 16 ? 12 : 16);
-  constexpr int ARS = (NW == 16 && TC == 16) ? 2 : 4;
-  constexpr int AD = ARS - 1;
-  static_assert(NP <= NT, "one piece per thread");
+  constexpr int NPA = STAGED ? KS * 4 * MB : 0;         // activation pieces (4 per row and k-block)
+  constexpr int P1 = NB + NM, P2 = P1 + NSC, P = P2 + NPA;
+  constexpr int SL = (P + NT - 1) / NT;                 // load slots per thread and stage
+  constexpr int DA = STAGED ? 0 : KPW;                  // direct activation loads per stage
+  constexpr int MOFF = NB * 16, SOFF = MOFF + NM * 16, AOFF = SOFF + NSC * 16;
+  constexpr int STAGE = AOFF + NPA * 16;
+  // Ring depth: at most ~56 loads in flight per wave (vmcnt counts to 63) and a
+  // register budget for the ring that leaves room for two workgroups per CU.  Even,
+  // so that ring slot i always uses LDS buffer i & 1 (consecutive stages must
+  // alternate buffers, also across the wrap from slot D-1 to slot 0).
+  constexpr int LPS = SL + DA;
+  constexpr int RING_VGPRS = NW <= 4 ? 96 : 64;
+  constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
+  static_assert(D >= 2 && D % 2 == 0, "even ring depth");
+  static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
 
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][STAGE];
-  __shared__ float red[NW / 2][16][TC + 1];
+  __shared__ float red[NW / 2 > 0 ? NW / 2 : 1][16][TC + 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -63,78 +81,84 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int chunk = n0 >> 6;
   const int g0 = (n0 & 63) >> 3;
 
-  // ---- this thread's piece: global byte offset = base + row * stride, row clamped ----
-  const uint8_t* pbase;
-  size_t pstride;
-  int prow;      // k-block (or scale group) of the piece within a stage
-  int pmaxrow;   // last valid k-block (or group)
-  int pper;      // rows per stage (KS for k-blocks, KS/4 for groups)
-  int plds;
-  if (tid < NB) {
-    const int kk = tid / BPK, w = tid % BPK;
-    if constexpr (VF == VAL4) {
-      pbase = static_cast<const uint8_t*>(a.B) + 8 * (size_t)n0 + 16 * w;
-      pstride = 8 * (size_t)N;
+  // ---- per-slot piece state: bytes at base + min(s*per + row0, rmax) * stride ----
+  const uint8_t* sbase[SL];
+  uint32_t sstride[SL], srow0[SL], sper[SL], srmax[SL], slds[SL];
+  bool szero[SL];  // activation piece: zero past the last k-block
+#pragma unroll
+  for (int q = 0; q < SL; q++) {
+    const int pc = cmin(tid + q * NT, P - 1);  // surplus lanes repeat the last piece
+    szero[q] = false;
+    if (pc < NB) {
+      const int kk = pc / BPK, w = pc % BPK;
+      constexpr int bpc = VF == VAL4 ? 8 : 6;  // packed bytes per column and k-block
+      sbase[q] = static_cast<const uint8_t*>(a.B) + bpc * (size_t)n0 + 16 * w;
+      sstride[q] = bpc * (uint32_t)N;
+      srow0[q] = kk;
+      sper[q] = KS;
+      srmax[q] = nkb - 1;
+      slds[q] = kk * BPK * 16 + 16 * w;
+    } else if (pc < P1) {
+      const int p = pc - NB, kk = p / MPK, w = p % MPK;
+      const uint8_t* mb = static_cast<const uint8_t*>(a.meta);
+      if constexpr (MF == META4) {
+        // two parts (units of the column pairs j>>1 = 0, 1), 2*TC bytes each
+        const int jbp = w / (MPK / 2), wp = w % (MPK / 2);
+        sbase[q] = mb + 256 * (size_t)chunk + 128 * jbp + 16 * g0 + 16 * wp;
+        sstride[q] = 4 * (uint32_t)N;
+        slds[q] = MOFF + kk * MPK * 16 + jbp * 2 * TC + 16 * wp;
+      } else if constexpr (TC == 64) {
+        // the whole 48-word group of the chunk
+        sbase[q] = mb + 192 * (size_t)chunk + 16 * w;
+        sstride[q] = 3 * (uint32_t)N;
+        slds[q] = MOFF + kk * MPK * 16 + 16 * w;
+      } else {
+        // rows (which, which+1) of the group, TC/2 words each starting at word p0
+        const int which = g0 >> 2, p0 = (4 * g0) & 15;
+        const int row = w / (TC / 8), wp = w % (TC / 8);
+        sbase[q] = mb + 192 * (size_t)chunk + 4 * (16 * (which + row) + p0) + 16 * wp;
+        sstride[q] = 3 * (uint32_t)N;
+        slds[q] = MOFF + kk * MPK * 16 + row * 2 * TC + 16 * wp;
+      }
+      srow0[q] = kk;
+      sper[q] = KS;
+      srmax[q] = nkb - 1;
+    } else if (pc < P2) {
+      const int p = pc - P1, gl = p / SPG, w = p % SPG;
+      sbase[q] = reinterpret_cast<const uint8_t*>(a.s) + 2 * (size_t)n0 + 16 * w;
+      sstride[q] = 2 * (uint32_t)N;
+      srow0[q] = gl;
+      sper[q] = KS / 4;
+      srmax[q] = ngroups - 1;
+      slds[q] = SOFF + gl * 2 * TC + 16 * w;
     } else {
-      pbase = static_cast<const uint8_t*>(a.B) + 6 * (size_t)n0 + 16 * w;
-      pstride = 6 * (size_t)N;
+      const int p = pc - P2, kk = p / (4 * MB), m = (p >> 2) % MB, u = p & 3;
+      const int mm = m < M ? m : M - 1;
+      sbase[q] = reinterpret_cast<const uint8_t*>(a.A) + 2 * (size_t)mm * K + 16 * u;
+      sstride[q] = 64;
+      srow0[q] = kk;
+      sper[q] = KS;
+      srmax[q] = nkb - 1;
+      slds[q] = AOFF + (kk * MB + m) * 64 + 16 * u;
+      szero[q] = true;
     }
-    prow = kk;
-    pmaxrow = nkb - 1;
-    pper = KS;
-    plds = kk * BPK * 16 + 16 * w;
-  } else if (tid < NB + NM) {
-    const int q = tid - NB, kk = q / MPK, w = q % MPK;
-    if constexpr (MF == META4) {
-      // two parts (units of the first / second column pair j>>1), 2*TC bytes each
-      const int jbp = w / (MPK / 2), wp = w % (MPK / 2);
-      pbase = static_cast<const uint8_t*>(a.meta) + 256 * (size_t)chunk + 128 * jbp + 16 * g0 + 16 * wp;
-      pstride = 4 * (size_t)N;
-      plds = BBYTES + kk * MPK * 16 + jbp * 2 * TC + 16 * wp;
-    } else if constexpr (TC == 64) {
-      // the whole 48-word group of the chunk
-      pbase = static_cast<const uint8_t*>(a.meta) + 192 * (size_t)chunk + 16 * w;
-      pstride = 3 * (size_t)N;
-      plds = BBYTES + kk * MPK * 16 + 16 * w;
-    } else {
-      // rows (which, which+1) of the group, TC/2 words each starting at word P0
-      const int which = g0 >> 2, p0 = (4 * g0) & 15;
-      const int row = w / (TC / 8), wp = w % (TC / 8);
-      pbase = static_cast<const uint8_t*>(a.meta) + 192 * (size_t)chunk + 4 * (16 * (which + row) + p0) + 16 * wp;
-      pstride = 3 * (size_t)N;
-      plds = BBYTES + kk * MPK * 16 + row * 2 * TC + 16 * wp;
-    }
-    prow = kk;
-    pmaxrow = nkb - 1;
-    pper = KS;
-  } else if (tid < NP) {
-    const int q = tid - NB - NM, gl = q / SPG, w = q % SPG;
-    pbase = reinterpret_cast<const uint8_t*>(a.s) + 2 * (size_t)n0 + 16 * w;
-    pstride = 2 * (size_t)N;
-    prow = gl;
-    pmaxrow = ngroups - 1;
-    pper = KS / 4;
-    plds = BBYTES + MBYTES + gl * 2 * TC + 16 * w;
-  } else {
-    pbase = reinterpret_cast<const uint8_t*>(a.zeros);
-    pstride = 0;
-    prow = 0;
-    pmaxrow = 0;
-    pper = 0;
-    plds = DUMMY + 16 * (tid - NP);
   }
-  auto load_piece = [&](int s) -> u32x4 {
-    int row = s * pper + prow;
-    row = row < pmaxrow ? row : pmaxrow;
-    return *reinterpret_cast<const u32x4*>(pbase + (size_t)row * pstride);
+  // Slot q of this wave holds pieces iff q*NT + 64*wave < P (uniform per wave).
+  auto slot_live = [&](int q) -> bool { return q < SL - 1 || (SL - 1) * NT + 64 * wave < P; };
+  // Activation pieces past the last k-block read the zero buffer (an address select:
+  // a select on the loaded value would wait for the load right away).
+  const uint8_t* zeros = reinterpret_cast<const uint8_t*>(a.zeros);
+  auto load_slot = [&](int q, int s) -> u32x4 {
+    const uint32_t row = (uint32_t)s * sper[q] + srow0[q];
+    const uint32_t r = row < srmax[q] ? row : srmax[q];
+    const uint8_t* p = sbase[q] + (uint64_t)r * sstride[q];
+    if (q * NT + NT > P2) {  // the slot may hold activation pieces
+      if (szero[q] && row > srmax[q]) p = zeros;
+    }
+    return *reinterpret_cast<const u32x4*>(p);
   };
 
   // ---- MFMA lane roles ----
-  // Lane group h covers dense groups 2h and 2h+1 of a k-block (k-space = dense K, so
-  // the activation operand is 16 contiguous bytes).  Group d of a column sits in word
-  // t = d mod 4 of the packed layout, as its first (d < 4) or second (d >= 4) nibble
-  // pair: lane group h reads words t0 = 2*(h&1) and t0+1 and takes nibble pair
-  // p = 2*blk + (h>>1), i.e. nibbles p and p+4.
   const int h = lane >> 4;
   const int rho = lane & 15;   // A row = column n0 + 16*cb + rho; B column = batch row
   const int gl = rho >> 3, blk = (rho >> 2) & 1, j = rho & 3;
@@ -143,39 +167,40 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int ehalf = h >> 1;                          // metadata int16: first/second 16 dense K
   const uint32_t nsh = 4u * (2u * blk + ehalf);      // nibble-pair shift in a value word
   const uint32_t msh = 8u * (h & 1);                 // index-byte shift in a metadata int16
-  const int m_act = rho;
-  const bool act_ok = m_act < M;
+  const int arow = rho & (MB - 1);                   // staged activation row of this lane
+  // direct activation operand: batch row rho (rows past M repeat row M-1)
+  const _Float16* abase = a.A + (size_t)(rho < M ? rho : M - 1) * K + 8 * h;
 
-  auto load_act = [&](int s, half8_t* dst) {
-#pragma unroll
-    for (int q = 0; q < KPW; q++) {
-      int kb = s * KS + wave * KPW + q;
-      const bool live = act_ok && kb < nkb;
-      const _Float16* ap = live ? a.A + (size_t)m_act * K + 32 * kb + 8 * h : a.zeros;
-      dst[q] = *reinterpret_cast<const half8_t*>(ap);
-    }
+  auto load_direct = [&](int s, int q) -> half8_t {
+    const int kb = s * KS + wave * KPW + q;  // uniform
+    const _Float16* p = kb < nkb ? abase + 32 * kb : a.zeros;
+    return *reinterpret_cast<const half8_t*>(p);
   };
 
-  float4_t acc[NCB];
+  // one accumulator per k-block of a wave's share (no MFMA dependency chains)
+  float4_t acc[KPW][NCB];
 #pragma unroll
-  for (int cb = 0; cb < NCB; cb++) acc[cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < KPW; q++)
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) acc[q][cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int s, const uint8_t* st, const half8_t* act) {
+  auto compute = [&](const uint8_t* st, const half8_t* dact) {
 #pragma unroll
     for (int q = 0; q < KPW; q++) {
       const int kk = wave * KPW + q;
-      if (s * KS + kk >= nkb) break;  // wave-uniform
+      half8_t act;
+      if constexpr (STAGED) act = *reinterpret_cast<const half8_t*>(st + AOFF + (kk * MB + arow) * 64 + 16 * h);
+      else act = dact[q];
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;
         const int wi0 = 16 * gt + 4 * t0 + j;  // words t0 and t0+1 of the tile's k-block row
         uint32_t w0, w1;
+        const uint8_t* rowp = st + kk * (BPK * 16);
         if constexpr (VF == VAL4) {
-          const uint8_t* rowp = st + kk * (BPK * 16);
           w0 = *reinterpret_cast<const uint32_t*>(rowp + 4 * wi0);
           w1 = *reinterpret_cast<const uint32_t*>(rowp + 4 * (wi0 + 4));
         } else {
-          const uint8_t* rowp = st + kk * (BPK * 16);
           const int b0 = 3 * wi0, b1 = 3 * (wi0 + 4);
           const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
@@ -194,20 +219,20 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         uint32_t idx;
         if constexpr (MF == META4) {
           const uint16_t md = *reinterpret_cast<const uint16_t*>(
-              st + BBYTES + kk * (MPK * 16) + jb * 2 * TC + 8 * (2 * gt + jj) + 2 * (blk + 2 * ehalf));
+              st + MOFF + kk * (MPK * 16) + jb * 2 * TC + 8 * (2 * gt + jj) + 2 * (blk + 2 * ehalf));
           idx = ((uint32_t)md >> msh) & 0xFFu;
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
           // (jb = 0) or high 24 bits of field "first" (g < 4) or "second" (g >= 4)
           // at position P = u mod 16, built from words (which, which+1).
-          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + BBYTES + kk * (MPK * 16));
+          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + MOFF + kk * (MPK * 16));
           uint32_t X, Y;
           int which;
           if constexpr (TC == 64) {
             which = gt >> 2;
-            const int P = (4 * gt + 2 * jj + ehalf) & 15;
-            X = mrow[16 * which + P];
-            Y = mrow[16 * (which + 1) + P];
+            const int Pw = (4 * gt + 2 * jj + ehalf) & 15;
+            X = mrow[16 * which + Pw];
+            Y = mrow[16 * (which + 1) + Pw];
           } else {
             which = g0 >> 2;
             const int pl = 4 * gt + 2 * jj + ehalf;
@@ -224,70 +249,91 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         }
         if constexpr (GROUPED) {
           const _Float16 sc =
-              *reinterpret_cast<const _Float16*>(st + BBYTES + MBYTES + (kk >> 2) * 2 * TC + 2 * (8 * gt + 2 * j + blk));
+              *reinterpret_cast<const _Float16*>(st + SOFF + (kk >> 2) * 2 * TC + 2 * (8 * gt + 2 * j + blk));
           aop = scale4(aop, sc);
         }
-        acc[cb] = smfmac32<0>(aop, act[q], acc[cb], idx);
+        acc[q][cb] = smfmac32<0>(aop, act, acc[q][cb], idx);
       }
     }
   };
 
-  // ---- pipeline ----
-  u32x4 wring[D];
-  half8_t aring[ARS][KPW];
+  // ---- pipeline: ring of D stages ----
+  // The prologue loads stages 0..D-1 and every full round of D stages loads the
+  // stages D later, all unconditionally (stages past the end re-read the last rows:
+  // the waits stay exact, which a conditional load would spoil).  The final round
+  // issues no loads.
+  u32x4 ring[D][SL];
+  half8_t dring[D][DA > 0 ? DA : 1];
 #pragma unroll
   for (int i = 0; i < D; i++) {
-    wring[i] = load_piece(i);
+#pragma unroll
+    for (int q = 0; q < SL; q++)
+      if (slot_live(q)) ring[i][q] = load_slot(q, i);
+#pragma unroll
+    for (int q = 0; q < DA; q++) dring[i][q] = load_direct(i, q);
     __builtin_amdgcn_sched_barrier(0);
   }
+  auto stage = [&](int i, bool reload, int s) {
+    uint8_t* st = lds[i & 1];
 #pragma unroll
-  for (int i = 0; i < AD; i++) {
-    load_act(i, aring[i]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  for (int base = 0; base < nst; base += D) {
-#pragma unroll
-    for (int i = 0; i < D; i++) {
-      const int s = base + i;
-      if (s >= nst) break;  // uniform
-      *reinterpret_cast<u32x4*>(&lds[i & 1][plds]) = wring[i];
-      wring[i] = load_piece(s + D);
-      load_act(s + AD, aring[(i + AD) % ARS]);
-      __syncthreads();
-      __builtin_amdgcn_sched_barrier(0);
-      compute(s, lds[i & 1], aring[i % ARS]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int q = 0; q < SL; q++) {
+      if (slot_live(q)) {
+        *reinterpret_cast<u32x4*>(st + slds[q]) = ring[i][q];
+        if (reload) ring[i][q] = load_slot(q, s + D);
+      }
     }
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st, dring[i]);
+    if (reload) {
+#pragma unroll
+      for (int q = 0; q < DA; q++) dring[i][q] = load_direct(s + D, q);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int base = 0;
+  for (; base + D < nst; base += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) stage(i, true, base + i);
   }
+#pragma unroll
+  for (int i = 0; i < D; i++)
+    if (base + i < nst) stage(i, false, base + i);  // uniform
 
-  // ---- reduce the NW waves pairwise in LDS (fixed order), wave 0 writes C ----
+#pragma unroll
+  for (int q = 1; q < KPW; q++)
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) acc[0][cb] += acc[q][cb];
+
+  // ---- reduce the NW waves pairwise in LDS (fixed order); wave 0 writes C ----
 #pragma unroll
   for (int half = NW / 2; half >= 1; half >>= 1) {
     if (wave >= half && wave < 2 * half) {
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) red[wave - half][rho][16 * cb + 4 * h + i] = acc[cb][i];
+        for (int i = 0; i < 4; i++) red[wave - half][rho][16 * cb + 4 * h + i] = acc[0][cb][i];
     }
     __syncthreads();
     if (wave < half) {
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[cb][i] += red[wave][rho][16 * cb + 4 * h + i];
+        for (int i = 0; i < 4; i++) acc[0][cb][i] += red[wave][rho][16 * cb + 4 * h + i];
     }
     __syncthreads();
   }
   if (wave == 0 && rho < M) {
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
+      const int n = n0 + 16 * cb + 4 * h;
+      half4_t o;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int n = n0 + 16 * cb + 4 * h + i;
-        _Float16 o = (_Float16)acc[cb][i];
-        if constexpr (!GROUPED) o = o * a.s[n];
-        a.C[(size_t)rho * N + n] = o;
+        o[i] = (_Float16)acc[0][cb][i];
+        if constexpr (!GROUPED) o[i] = o[i] * a.s[n + i];
       }
+      *reinterpret_cast<half4_t*>(a.C + (size_t)rho * N + n) = o;
     }
   }
 }

@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <initializer_list>
 #include <map>
 #include <mutex>
 #include <string>
@@ -415,50 +416,73 @@ hipError_t launch_v(const GemmArgs& a, int bb, bool grouped, dim3 grid, hipStrea
   return launch_t<4, false, VF, MF>(a, grid, stream);
 }
 
-// Column-tile width of the decode kernel: the widest tile (fewest re-reads of the
-// activations) that still gives every compute unit at least one workgroup.
-int decode_tile_cols(int N, int cus) {
-  if (N / 64 >= cus) return 64;
-  if (N / 32 >= cus) return 32;
-  return 16;
+// Integer knob from the environment, read once per call site; `fallback` when unset
+// or not one of `allowed`.
+int env_choice(const char* name, std::initializer_list<int> allowed, int fallback) {
+  const char* e = getenv(name);
+  if (!e) return fallback;
+  const int x = atoi(e);
+  for (int v : allowed)
+    if (v == x) return x;
+  return fallback;
 }
 
-// Waves per decode workgroup (MARLIN_HIP_DECODE_WAVES overrides; read once).
-int decode_waves() {
-  static const int v = [] {
-    const char* e = getenv("MARLIN_HIP_DECODE_WAVES");
-    const int x = e ? atoi(e) : 0;
-    return (x == 4 || x == 8 || x == 16) ? x : 8;
-  }();
-  return v;
+// Column-tile width and waves per workgroup of the decode kernel, from measured
+// single-call times on MI355X (Llama-2-7B shapes, M = 1): wide grids (N/32 at least
+// twice the CUs) run best as 32-column tiles of 4 waves, mid-size N as 64-column
+// tiles of 8 waves, and N around the CU count as 16-column tiles of 8 waves.
+// MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES override.
+struct DecodeShape {
+  int tc, nw;
+};
+DecodeShape decode_shape(int N, int cus) {
+  static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
+  static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
+  DecodeShape d;
+  if (N / 32 >= 2 * cus) d = {32, 4};
+  else if (4 * (N / 64) >= 3 * cus) d = {64, 8};
+  else d = {16, 8};
+  if (forced_tc) d.tc = forced_tc;
+  if (forced_nw) d.nw = forced_nw;
+  return d;
+}
+
+// Padded batch of the decode kernel: 1, 4 (activations staged through LDS) or 16
+// (loaded straight into the MFMA operand).
+int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : 16); }
+
+template <int TC, int NW, int MB, bool GROUPED>
+void launch_decode_mb(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
+  const dim3 grid(a.N / TC), block(64 * NW);
+  if (vf == VAL3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4>), grid, block, 0, stream, a);
+  else if (mf == META3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META3>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META4>), grid, block, 0, stream, a);
 }
 
 template <int TC, int NW, bool GROUPED>
 void launch_decode_nw(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
-  const dim3 grid(a.N / TC), block(64 * NW);
-  if (vf == VAL3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, GROUPED, VAL3, META4>), grid, block, 0, stream, a);
-  else if (mf == META3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, GROUPED, VAL4, META3>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, GROUPED, VAL4, META4>), grid, block, 0, stream, a);
+  const int mb = decode_batch(a.M);
+  if (mb == 1) launch_decode_mb<TC, NW, 1, GROUPED>(a, vf, mf, stream);
+  else if (mb == 4) launch_decode_mb<TC, NW, 4, GROUPED>(a, vf, mf, stream);
+  else launch_decode_mb<TC, NW, 16, GROUPED>(a, vf, mf, stream);
 }
 
 template <int TC, bool GROUPED>
-hipError_t launch_decode_t(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
-  const int nw = decode_waves();
+hipError_t launch_decode_t(const GemmArgs& a, int nw, int vf, int mf, hipStream_t stream) {
   if (nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, vf, mf, stream);
-  else if (nw == 16) launch_decode_nw<TC, 16, GROUPED>(a, vf, mf, stream);
   else launch_decode_nw<TC, 8, GROUPED>(a, vf, mf, stream);
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const GemmArgs& a, int tc, int vf, int mf, bool grouped, hipStream_t stream) {
+hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool grouped, hipStream_t stream) {
   if (grouped) {
-    if (tc == 64) return launch_decode_t<64, true>(a, vf, mf, stream);
-    if (tc == 32) return launch_decode_t<32, true>(a, vf, mf, stream);
-    return launch_decode_t<16, true>(a, vf, mf, stream);
+    if (d.tc == 64) return launch_decode_t<64, true>(a, d.nw, vf, mf, stream);
+    if (d.tc == 32) return launch_decode_t<32, true>(a, d.nw, vf, mf, stream);
+    return launch_decode_t<16, true>(a, d.nw, vf, mf, stream);
   }
-  if (tc == 64) return launch_decode_t<64, false>(a, vf, mf, stream);
-  if (tc == 32) return launch_decode_t<32, false>(a, vf, mf, stream);
-  return launch_decode_t<16, false>(a, vf, mf, stream);
+  if (d.tc == 64) return launch_decode_t<64, false>(a, d.nw, vf, mf, stream);
+  if (d.tc == 32) return launch_decode_t<32, false>(a, d.nw, vf, mf, stream);
+  return launch_decode_t<16, false>(a, d.nw, vf, mf, stream);
 }
 
 // Shape/tile validation with the reference's rules and error codes
@@ -527,8 +551,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
       return err;
     }
-    const int tc = decode_tile_cols(N, sms);
-    hipError_t e = launch_decode(d, tc, vf, mf, groupsize != -1, stream);
+    hipError_t e = launch_decode(d, decode_shape(N, sms), vf, mf, groupsize != -1, stream);
     if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
     if (e != hipSuccess) {
       set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
