@@ -77,7 +77,20 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int nkb = K >> 5;
   const int ngroups = (nkb + 3) >> 2;
   const int nst = (nkb + KS - 1) / KS;
-  const int n0 = blockIdx.x * TC;
+  // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8 XCDs
+  // (block b runs on XCD b % 8) and each XCD has its own L2.  The SUB = 64/TC tiles of
+  // one 64-column chunk share 128-byte lines of metadata and scales (a tile's packed
+  // values are whole lines), so they go to blocks b = 8*(SUB*q + s) + x, which all
+  // sit on XCD x: each line is fetched from HBM once instead of once per tile.
+  constexpr int SUB = 64 / TC;
+  int tile = blockIdx.x;
+  if constexpr (SUB > 1) {
+    if (gridDim.x % (8 * SUB) == 0) {
+      const int x = tile & 7, jx = tile >> 3;
+      tile = (8 * (jx / SUB) + x) * SUB + jx % SUB;
+    }
+  }
+  const int n0 = tile * TC;
   const int chunk = n0 >> 6;
   const int g0 = (n0 & 63) >> 3;
 
@@ -171,6 +184,20 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // direct activation operand: batch row rho (rows past M repeat row M-1)
   const _Float16* abase = a.A + (size_t)(rho < M ? rho : M - 1) * K + 8 * h;
 
+  // Per-lane LDS byte offsets of this wave's first k-block and column block; the
+  // k-block (q), column block (cb) and buffer parts are immediates.
+  const int kw = wave * KPW;                          // first k-block of this wave in a stage
+  const uint32_t o_val = kw * (BPK * 16) + (VF == VAL4 ? 4 * (16 * gl + 4 * t0 + j) : 0);
+  const int wi_lane = 16 * gl + 4 * t0 + j;           // 3-bit values: word index without cb
+  const uint32_t o_meta = MOFF + kw * (MPK * 16) + jb * 2 * TC + 8 * (2 * gl + jj) + 2 * (blk + 2 * ehalf);
+  const uint32_t o_mrow = MOFF + kw * (MPK * 16);
+  const uint32_t o_scale = SOFF + (kw >> 2) * 2 * TC + 2 * (8 * gl + 2 * j + blk);  // same group for all q
+  const uint32_t o_act = AOFF + (kw * MB + arow) * 64 + 16 * h;
+  // Dequant constants held in VGPRs, so that mask-and-or is one v_and_or_b32.
+  uint32_t kMask, kMagic;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
+
   auto load_direct = [&](int s, int q) -> half8_t {
     const int kb = s * KS + wave * KPW + q;  // uniform
     const _Float16* p = kb < nkb ? abase + 32 * kb : a.zeros;
@@ -187,29 +214,29 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   auto compute = [&](const uint8_t* st, const half8_t* dact) {
 #pragma unroll
     for (int q = 0; q < KPW; q++) {
-      const int kk = wave * KPW + q;
       half8_t act;
-      if constexpr (STAGED) act = *reinterpret_cast<const half8_t*>(st + AOFF + (kk * MB + arow) * 64 + 16 * h);
+      if constexpr (STAGED) act = *reinterpret_cast<const half8_t*>(st + o_act + q * MB * 64);
       else act = dact[q];
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;
-        const int wi0 = 16 * gt + 4 * t0 + j;  // words t0 and t0+1 of the tile's k-block row
         uint32_t w0, w1;
-        const uint8_t* rowp = st + kk * (BPK * 16);
         if constexpr (VF == VAL4) {
-          w0 = *reinterpret_cast<const uint32_t*>(rowp + 4 * wi0);
-          w1 = *reinterpret_cast<const uint32_t*>(rowp + 4 * (wi0 + 4));
+          // words t0 and t0+1 of the tile's k-block row
+          const uint8_t* vp = st + o_val + q * (BPK * 16) + 128 * cb;
+          w0 = *reinterpret_cast<const uint32_t*>(vp);
+          w1 = *reinterpret_cast<const uint32_t*>(vp + 16);
         } else {
-          const int b0 = 3 * wi0, b1 = 3 * (wi0 + 4);
+          const uint8_t* rowp = st + o_val + q * (BPK * 16);
+          const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
           const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
           w0 = spread3(__builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3)) & 0xFFFFFFu);
           w1 = spread3(__builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3)) & 0xFFFFFFu);
         }
         // values: nibble pairs of words t0, t0+1 -> {g_2h slot0, slot1, g_2h+1 slot0, slot1}
-        const uint32_t x0 = ((w0 >> nsh) & 0x000F000Fu) | 0x64006400u;
-        const uint32_t x1 = ((w1 >> nsh) & 0x000F000Fu) | 0x64006400u;
+        const uint32_t x0 = ((w0 >> nsh) & kMask) | kMagic;
+        const uint32_t x1 = ((w1 >> nsh) & kMask) | kMagic;
         constexpr float zp = VF == VAL4 ? 1032.0f : 1028.0f;  // 1024 + zero point
         const half2_t v0 = __builtin_bit_cast(half2_t, x0) - (half2_t){(_Float16)zp, (_Float16)zp};
         const half2_t v1 = __builtin_bit_cast(half2_t, x1) - (half2_t){(_Float16)zp, (_Float16)zp};
@@ -218,14 +245,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         // nibbles of dense groups 2h and 2h+1
         uint32_t idx;
         if constexpr (MF == META4) {
-          const uint16_t md = *reinterpret_cast<const uint16_t*>(
-              st + MOFF + kk * (MPK * 16) + jb * 2 * TC + 8 * (2 * gt + jj) + 2 * (blk + 2 * ehalf));
+          const uint16_t md = *reinterpret_cast<const uint16_t*>(st + o_meta + q * (MPK * 16) + 32 * cb);
           idx = ((uint32_t)md >> msh) & 0xFFu;
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
           // (jb = 0) or high 24 bits of field "first" (g < 4) or "second" (g >= 4)
           // at position P = u mod 16, built from words (which, which+1).
-          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + MOFF + kk * (MPK * 16));
+          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + q * (MPK * 16));
           uint32_t X, Y;
           int which;
           if constexpr (TC == 64) {
@@ -248,8 +274,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           idx = ((lut >> (4u * ca)) & 15u) | (((lut >> (4u * cbv)) & 15u) << 4);
         }
         if constexpr (GROUPED) {
-          const _Float16 sc =
-              *reinterpret_cast<const _Float16*>(st + SOFF + (kk >> 2) * 2 * TC + 2 * (8 * gt + 2 * j + blk));
+          const _Float16 sc = *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
           aop = scale4(aop, sc);
         }
         acc[q][cb] = smfmac32<0>(aop, act, acc[q][cb], idx);

@@ -429,9 +429,9 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 
 // Column-tile width and waves per workgroup of the decode kernel, from measured
 // single-call times on MI355X (Llama-2-7B shapes, M = 1): wide grids (N/32 at least
-// twice the CUs) run best as 32-column tiles of 4 waves, mid-size N as 64-column
-// tiles of 8 waves, and N around the CU count as 16-column tiles of 8 waves.
-// MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES override.
+// twice the CUs) run best as 32-column tiles of 4 waves, everything narrower as
+// 16-column tiles of 8 waves.  MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES
+// override.
 struct DecodeShape {
   int tc, nw;
 };
@@ -440,7 +440,6 @@ DecodeShape decode_shape(int N, int cus) {
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   DecodeShape d;
   if (N / 32 >= 2 * cus) d = {32, 4};
-  else if (4 * (N / 64) >= 3 * cus) d = {64, 8};
   else d = {16, 8};
   if (forced_tc) d.tc = forced_tc;
   if (forced_nw) d.nw = forced_nw;

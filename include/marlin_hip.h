@@ -15,11 +15,16 @@
  * pointers): A M*K halves, B K*N/16 int32, meta K*N/16 int16, C M*N halves,
  * s (K/128 or 1)*N halves.
  *
- * Split-K scratch (fp32 partials and arrival counters) is allocated by the library
- * once per device, grown on demand outside stream capture, and shared by all
- * streams: GEMM calls that overlap in time on one device race (serialise them on
- * one stream, as with the reference's shared workspace).  The counters carry a
- * per-launch tag, so no buffer needs to be zeroed by the caller.
+ * Decode calls (prob_n = M <= 16) use no scratch: one workgroup owns each output
+ * column tile over the whole K.  For M > 16 the planner may split K; the split-K
+ * scratch (fp32 partials and arrival counters) is uncached device memory that the
+ * library allocates once per device, grows on demand outside stream capture (a
+ * grow during capture is refused with code 3) and never frees.  The counters are
+ * zeroed at allocation and each is returned to zero by the last workgroup that
+ * arrives on it, so no buffer needs to be zeroed by the caller.  The scratch is
+ * shared by all streams of a device: split-K calls that overlap in time on one
+ * device race (serialise them on one stream, as with the reference's shared
+ * workspace).
  */
 #ifndef MARLIN_HIP_H
 #define MARLIN_HIP_H
