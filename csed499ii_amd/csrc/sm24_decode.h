@@ -58,11 +58,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int MOFF = NB * 16, SOFF = MOFF + NM * 16, AOFF = SOFF + NSC * 16;
   constexpr int STAGE = AOFF + NPA * 16;
   // Ring depth: at most ~56 loads in flight per wave (vmcnt counts to 63) and a
-  // register budget for the ring that leaves room for two workgroups per CU.  Even,
-  // so that ring slot i always uses LDS buffer i & 1 (consecutive stages must
-  // alternate buffers, also across the wrap from slot D-1 to slot 0).
+  // register budget for the ring that keeps the kernel at <= 128 VGPRs (two
+  // 8-wave or four 4-wave workgroups per CU).  Even, so that ring slot i always
+  // uses LDS buffer i & 1 (consecutive stages must alternate buffers, also across
+  // the wrap from slot D-1 to slot 0).
   constexpr int LPS = SL + DA;
-  constexpr int RING_VGPRS = NW <= 4 ? 96 : 64;
+  constexpr int RING_VGPRS = STAGED ? 48 : 80;
   constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
@@ -157,7 +158,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     }
   }
   // Slot q of this wave holds pieces iff q*NT + 64*wave < P (uniform per wave).
-  auto slot_live = [&](int q) -> bool { return q < SL - 1 || (SL - 1) * NT + 64 * wave < P; };
+  // Slot 0 is loaded by every wave (a wave without pieces repeats the last one): a
+  // load under a branch leaves the compiler no exact wait count, and with only
+  // conditional loads in flight every stage would wait for all of them.
+  constexpr bool kLastAll = (SL - 1) * NT + 64 * (NW - 1) < P;  // every wave has a piece in slot SL-1
+  auto slot_live = [&](int q) -> bool {
+    return q == 0 || q < SL - 1 || kLastAll || (SL - 1) * NT + 64 * wave < P;
+  };
   // Activation pieces past the last k-block read the zero buffer (an address select:
   // a select on the loaded value would wait for the load right away).
   const uint8_t* zeros = reinterpret_cast<const uint8_t*>(a.zeros);
@@ -180,7 +187,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int ehalf = h >> 1;                          // metadata int16: first/second 16 dense K
   const uint32_t nsh = 4u * (2u * blk + ehalf);      // nibble-pair shift in a value word
   const uint32_t msh = 8u * (h & 1);                 // index-byte shift in a metadata int16
-  const int arow = rho & (MB - 1);                   // staged activation row of this lane
+  const int arow = rho & (MB - 1);                   // staged activation row (lanes rho < MB)
   // direct activation operand: batch row rho (rows past M repeat row M-1)
   const _Float16* abase = a.A + (size_t)(rho < M ? rho : M - 1) * K + 8 * h;
 
@@ -211,12 +218,23 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[q][cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
+  half8_t sact[KPW];  // staged activation operands (lanes rho >= MB never reload)
+#pragma unroll
+  for (int q = 0; q < KPW; q++) sact[q] = (half8_t){};
+
   auto compute = [&](const uint8_t* st, const half8_t* dact) {
 #pragma unroll
     for (int q = 0; q < KPW; q++) {
       half8_t act;
-      if constexpr (STAGED) act = *reinterpret_cast<const half8_t*>(st + o_act + q * MB * 64);
-      else act = dact[q];
+      if constexpr (STAGED) {
+        // Only lanes of real batch rows read the staged row; the other lanes' MFMA
+        // columns are never stored, so their operand keeps whatever the register
+        // held (LDS reads are paid per active lane).
+        if (rho < MB) sact[q] = *reinterpret_cast<const half8_t*>(st + o_act + q * MB * 64);
+        act = sact[q];
+      } else {
+        act = dact[q];
+      }
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;

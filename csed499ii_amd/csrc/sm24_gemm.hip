@@ -428,19 +428,23 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 }
 
 // Column-tile width and waves per workgroup of the decode kernel, from measured
-// single-call times on MI355X (Llama-2-7B shapes, M = 1): wide grids (N/32 at least
-// twice the CUs) run best as 32-column tiles of 4 waves, everything narrower as
-// 16-column tiles of 8 waves.  MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES
-// override.
+// single-call times on MI355X (Llama-2-7B shapes, M in {1, 4, 8, 16}).  Tiles of
+// 16 columns give the most workgroups; wider tiles re-read the activation rows
+// fewer times, which pays once M > 1 and the grid still covers the CUs: 32-column
+// tiles when N/32 is at least twice the CU count, 64-column tiles when N/64 is at
+// least half of it.  MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES override.
 struct DecodeShape {
   int tc, nw;
 };
-DecodeShape decode_shape(int N, int cus) {
+DecodeShape decode_shape(int M, int N, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   DecodeShape d;
-  if (N / 32 >= 2 * cus) d = {32, 4};
-  else d = {16, 8};
+  const bool wide32 = N / 32 >= 2 * cus;
+  if (M == 1) d = {wide32 ? 32 : 16, 8};
+  else if (wide32) d = {32, 4};
+  else if (2 * (N / 64) >= cus) d = {64, 8};
+  else d = {16, M <= 4 ? 8 : 4};
   if (forced_tc) d.tc = forced_tc;
   if (forced_nw) d.nw = forced_nw;
   return d;
@@ -550,7 +554,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
       return err;
     }
-    hipError_t e = launch_decode(d, decode_shape(N, sms), vf, mf, groupsize != -1, stream);
+    hipError_t e = launch_decode(d, decode_shape(M, N, sms), vf, mf, groupsize != -1, stream);
     if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
     if (e != hipSuccess) {
       set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
