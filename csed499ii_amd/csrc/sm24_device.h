@@ -113,6 +113,11 @@ struct GemmArgs {
   uint32_t* counters;  // [gridDim.z][gridDim.x] arrival counters, zero between launches
 };
 
+// Large-M kernel (sm24_prefill.hip): output columns per workgroup tile (N must be a
+// multiple) and its launcher.
+constexpr int kPreTileCols = 512;
+hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream);
+
 template <int ABID>
 __device__ __forceinline__ float4_t smfmac32(half4_t a, half8_t b, float4_t c, uint32_t idx) {
   return __builtin_amdgcn_smfmac_f32_16x16x32_f16(a, b, c, (int)idx, 0, ABID);

@@ -488,6 +488,18 @@ hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool 
   return launch_decode_t<16, false>(a, d.nw, vf, mf, stream);
 }
 
+// Large-M path (sm24_prefill_kernel): 4-bit values and metadata, N a multiple of its
+// 512-column tile and K of its 64-deep k-step, from MARLIN_HIP_PREFILL_MIN_M rows
+// (default 256) up.
+bool prefill_fits(int M, int N, int K, int vf, int mf) {
+  static const int min_m = [] {
+    const char* e = getenv("MARLIN_HIP_PREFILL_MIN_M");
+    const int x = e ? atoi(e) : 0;
+    return x > 16 ? x : 256;
+  }();
+  return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 64 == 0;
+}
+
 // Shape/tile validation with the reference's rules and error codes
 // (marlin_cuda_kernel_nm.cu:760-823).
 int validate(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, int thread_m) {
@@ -555,6 +567,25 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       return err;
     }
     hipError_t e = launch_decode(d, decode_shape(M, N, sms), vf, mf, groupsize != -1, stream);
+    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+    if (e != hipSuccess) {
+      set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
+      return MARLIN_HIP_ERR_LAUNCH;
+    }
+    return MARLIN_HIP_OK;
+  }
+  if (prefill_fits(M, N, K, vf, mf)) {
+    GemmArgs p{};
+    p.A = static_cast<const _Float16*>(A);
+    p.B = B;
+    p.meta = meta;
+    p.s = static_cast<const _Float16*>(s);
+    p.C = static_cast<_Float16*>(C);
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.splits = 1;
+    hipError_t e = launch_prefill(p, groupsize != -1, stream);
     if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
     if (e != hipSuccess) {
       set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));

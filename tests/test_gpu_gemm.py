@@ -130,6 +130,17 @@ def test_decode_sweep_full_size_slices(K, N, M):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"{K}x{N} M={M} slice {c0}")
 
 
+@pytest.mark.parametrize("M,N,K,g", [(256, 512, 128, 128), (300, 1024, 256, -1), (257, 512, 192, -1),
+                                     (384, 1536, 512, 128), (640, 2048, 1024, 128)])
+def test_prefill_kernel_shapes(M, N, K, g):
+    """The large-M kernel: ragged row tiles, 1-3 k-steps, per-column and grouped
+    scales, several column tiles (every XCD ordering branch)."""
+    wt, A = _problem(M, N, K, g, 900 + M + K)
+    C = _run(wt, A)
+    _check(wt, A, C, f"prefill M={M} N={N} K={K} g={g}")
+    assert torch.equal(_run(wt, A), C), "repeated calls differ"
+
+
 @pytest.mark.parametrize("M", [512])
 def test_prefill_shape_slices(M):
     wt, A = _problem(M, 8192, 8192, 128, 31)
