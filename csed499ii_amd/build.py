@@ -43,12 +43,8 @@ def compile_flags() -> list[str]:
     ]
 
 
-# Per-source extra flags.  The large-M kernel keeps 256 fp32 accumulators per lane;
-# selecting the VGPR form of its MFMAs lets the register allocator place them without
-# spilling (the default form spills ~330 bytes per lane to scratch).
-EXTRA_FLAGS = {
-    "sm24_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-}
+# Per-source extra flags (none at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
 
 # hipcc's host pass does not know the packed-fp32 target feature: drop that noise.
 _NOISE = ("packed-fp32-ops", "is not a recognized feature")

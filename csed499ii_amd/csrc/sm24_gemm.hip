@@ -497,7 +497,8 @@ bool prefill_fits(int M, int N, int K, int vf, int mf) {
     const int x = e ? atoi(e) : 0;
     return x > 16 ? x : 256;
   }();
-  return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 64 == 0;
+  return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 128 == 0 &&
+         (long long)M * K < (1LL << 31);
 }
 
 // Shape/tile validation with the reference's rules and error codes

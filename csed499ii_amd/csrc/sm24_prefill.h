@@ -1,30 +1,35 @@
 // Prefill-sized (large M) 2:4 INT4 x FP16 GEMM for gfx950, MFMA-bound.
 //
-// Workgroup tile: 512 output columns (8 chunks of 64) x 128 batch rows, 4 waves; wave
-// w owns chunks 2w, 2w+1 (128 columns) for all 128 rows, so every wave holds
-// 2 chunks x 4 fragments x 8 batch blocks of v_smfmac_f32_16x16x64_f16 accumulators
-// (256 registers).  K advances in steps of 64 (two 32-deep k-blocks).
+// Workgroup tile: 512 output columns (8 chunks of 64) x 128 batch rows, 4 waves, one
+// per SIMD; wave w owns chunks 2w, 2w+1 (128 columns) for all 128 rows as 4 x 4
+// v_smfmac_f32_32x32x32_f16 accumulators (256 AGPRs).  K advances in steps of 64 (two
+// 32-deep k-blocks); one k-step is 32 MFMAs per wave.
 //
-// Operand routes, chosen for the per-CU budgets measured on MI355X (LDS ~128 B/clk,
-// ~16 cycles per 16-byte load instruction, 16 cycles per smfmac):
-//  * activations: cooperative 16-byte loads -> registers -> LDS (two buffers), each
-//    row stored in the MFMA's k order; every wave reads its 8 B fragments once per
-//    k-step and uses each with 8 weight fragments;
-//  * packed values: straight from global into registers, one 16-byte load per lane,
-//    chunk and k-block (covering the lane's 4 fragments), two k-steps ahead;
-//  * metadata: cooperative 8-byte loads of both k-blocks' units, transposed once per
-//    column into the index halfword each lane needs (an LDS table of 4 KiB);
-//  * scales: one 16-byte load per lane and chunk (the 4 fragments' scales).
+// Why 32x32x32.  Measured on MI355X with one wave per SIMD: an smfmac keeps the
+// SIMD's VALU issue busy for most of its own duration (13 of ~17 cycles for
+// 16x16x64), so VALU work overlaps an MFMA only up to ~1 instruction per 16x16x64
+// but ~5 per 32x32x32, which reads the same operand registers for twice the flops.
+// Dequantization costs 13 VALU instructions per 8-value weight fragment; with
+// 32x32x32 the k-step needs ~3.6 VALU instructions per MFMA, inside that budget.
 //
-// MFMA k order.  Within a 64-deep k-step, A lane group h holds MFMA groups 4h..4h+3
-// = real groups (k-block 0, group h), (0, h+4), (1, h), (1, h+4): exactly the
-// nibbles of the packed word (k-block, g8, t = h, j) for one column.  Activation
-// rows are stored permuted the same way (real group (kb, g) at MFMA group
-// g < 4 ? 4g + 2kb : 4(g-4) + 1 + 2kb), so a B lane's k-ranges [8h, 8h+8) and
-// [32+8h, 32+8h+8) are 16 contiguous bytes each.
+// Operand routes (all global reads are LDS-DMA: no staging registers, no staging
+// VALU; a ring of 4 k-steps, filled 3 steps ahead, one barrier per k-step):
+//  * activations: 128 rows x 128 bytes per k-step; 16-byte pieces stored with the
+//    logical slot XOR ((row >> 1) & 7) so that the B-fragment reads are free of bank
+//    conflicts; a B lane (row, h) reads the 32 contiguous bytes of k 16h..16h+15;
+//  * packed values, metadata, scales: the raw global layout of each wave's own 2
+//    chunks (512 + 256 + 128 bytes per chunk and k-step), read per lane as needed.
 //
-// Fragment f (0..3) of a chunk holds columns 8*g8 + 4*blk + f, row rho = 2*g8 + blk,
-// so a lane's four fragments read four consecutive packed words (j = f).
+// MFMA k order.  For a 32-deep k-block, A lane group h (lanes 32h..32h+31) holds MFMA
+// groups 4h..4h+3 = real groups 2h, 2h+1, 2h+4, 2h+5, which makes:
+//  * B lane group h's k-ranges (MFMA k 8h+[0,8) and 16+8h+[0,8)) the real k 16h..16h+15;
+//  * the A values the nibbles of the packed words (g8, t = 2h, j) and (g8, 2h+1, j):
+//    column half 0 (n) in bytes 0, 2 and half 1 (n+4) in bytes 1, 3 of each word;
+//  * the index halfword of half hf = [byte h of m(n',e0), byte h of m(n',e1)] with
+//    n' = n + 4hf, so one v_perm of the metadata unit gives both halves' indices
+//    (selected by abid).
+// A row rho (0..31) of fragment (chunk c, half hf) is output column
+// 64c + 8*(rho >> 2) + 4*hf + (rho & 3).
 #pragma once
 #include "sm24_device.h"
 
@@ -35,49 +40,72 @@ struct IntC {
   static constexpr int value = V;
 };
 
-constexpr int kPreRows = 128;   // batch rows per tile
-constexpr int kPreChunks = 8;   // 64-column chunks per tile
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kPreRows = 128;  // batch rows per tile
+constexpr int kPreChunks = 8;  // 64-column chunks per tile
 static_assert(64 * kPreChunks == kPreTileCols, "tile width");
-constexpr int kPreRS = 144;     // LDS bytes per activation row (128 + 16: conflict-free b128 reads)
+constexpr int kPreRing = 4;                        // k-steps resident in LDS
+constexpr int kPreActB = kPreRows * 128;           // activation bytes of one k-step
+constexpr int kPreWB = kPreChunks * 2 * 512;       // packed values of one k-step
+constexpr int kPreMB = kPreChunks * 2 * 256;       // metadata of one k-step
+constexpr int kPreSB = kPreChunks * 128;           // scales of one k-step
+constexpr int kPreActOff = 0;
+constexpr int kPreWOff = kPreActOff + kPreRing * kPreActB;
+constexpr int kPreMOff = kPreWOff + kPreRing * kPreWB;
+constexpr int kPreSOff = kPreMOff + kPreRing * kPreMB;
+constexpr int kPreLdsBytes = kPreSOff + kPreRing * kPreSB;
 
-// Real group (kb, g) of a 64-deep k-step -> MFMA group.
-__device__ __forceinline__ int pre_mgroup(int kb, int g) { return g < 4 ? 4 * g + 2 * kb : 4 * (g - 4) + 1 + 2 * kb; }
+// v_smfmac_f32_32x32x32_f16 with the accumulator in AGPRs; ABID selects the index
+// halfword.  Written as inline assembly because, for the intrinsic, the compiler
+// splits 256 accumulator registers between VGPRs and AGPRs and copies them around
+// the MFMAs.  Assembly takes the MFMA out of the compiler's hazard tracking, so the
+// kernel keeps the gfx950 rules by construction: an operand VGPR written by a VALU
+// instruction is read at least two instructions later (operands come from LDS
+// loads, which s_waitcnt covers, or were produced a k-step earlier), and the
+// accumulators are read only after pre_mfma_drain.
+template <int ABID>
+__device__ __forceinline__ void pre_smfmac(f32x16& c, half8_t a, half16_t b, uint32_t idx) {
+  if constexpr (ABID == 0)
+    asm volatile("v_smfmac_f32_32x32x32_f16 %0, %1, %2, %3" : "+a"(c) : "v"(a), "v"(b), "v"(idx));
+  else
+    asm volatile("v_smfmac_f32_32x32x32_f16 %0, %1, %2, %3 abid:1" : "+a"(c) : "v"(a), "v"(b), "v"(idx));
+}
 
-// 4x4 nibble transpose of the metadata of one column pair.  x0, y0: k-block 0 words
-// {m(n,e0) | m(n+4,e0) << 16}, {m(n,e1) | m(n+4,e1) << 16}; x1, y1: k-block 1.
-// Returns, for column n (lo) and n+4 (hi), the index halfwords of lane groups h = 0..3:
-// idx_h = m(kb0,e0)[h] | m(kb0,e1)[h] << 4 | m(kb1,e0)[h] << 8 | m(kb1,e1)[h] << 12.
-__device__ __forceinline__ void pre_meta_transpose(uint32_t x0, uint32_t y0, uint32_t x1, uint32_t y1,
-                                                   u32x2& lo, u32x2& hi) {
-  // even / odd nibbles to separate bytes, then pair the e0/e1 nibbles of a byte
-  const uint32_t ab_e = (x0 & 0x0F0F0F0Fu) | ((y0 & 0x0F0F0F0Fu) << 4);         // [h0, h2, h0', h2'] of kb0
-  const uint32_t ab_o = ((x0 >> 4) & 0x0F0F0F0Fu) | (y0 & 0xF0F0F0F0u);         // [h1, h3, h1', h3'] of kb0
-  const uint32_t cd_e = (x1 & 0x0F0F0F0Fu) | ((y1 & 0x0F0F0F0Fu) << 4);
-  const uint32_t cd_o = ((x1 >> 4) & 0x0F0F0F0Fu) | (y1 & 0xF0F0F0F0u);
-  // halfword h of column n = [ab byte, cd byte] with byte h/2 of the even (h even)
-  // or odd (h odd) word; v_perm_b32 selector bytes: 0-3 = second operand, 4-7 = first.
-  const uint32_t e = __builtin_amdgcn_perm(cd_e, ab_e, 0x05010400u);  // [ab_e.b0, cd_e.b0, ab_e.b1, cd_e.b1]
-  const uint32_t o = __builtin_amdgcn_perm(cd_o, ab_o, 0x05010400u);
-  const uint32_t e2 = __builtin_amdgcn_perm(cd_e, ab_e, 0x07030602u);  // bytes 2, 3: column n+4
-  const uint32_t o2 = __builtin_amdgcn_perm(cd_o, ab_o, 0x07030602u);
-  // words: [h0 | h1 << 16, h2 | h3 << 16]
-  lo.x = __builtin_amdgcn_perm(o, e, 0x05040100u);
-  lo.y = __builtin_amdgcn_perm(o, e, 0x07060302u);
-  hi.x = __builtin_amdgcn_perm(o2, e2, 0x05040100u);
-  hi.y = __builtin_amdgcn_perm(o2, e2, 0x07060302u);
+// Wait states between the last MFMA and the first read of its result.
+__device__ __forceinline__ void pre_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+
+// LDS-DMA: every lane copies 16 (4) bytes from base + voff to LDS byte address
+// lds + 16 (4) * lane.  Tracked by vmcnt, like any global load.
+__device__ __forceinline__ void pre_dma16(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void pre_dma4(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
+// Start of a k-step: this wave's DMAs except the last NDMA issued have landed, its
+// LDS reads are complete; then the workgroup meets.
+template <int NDMA>
+__device__ __forceinline__ void pre_step_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(NDMA) : "memory");
 }
 
 template <bool GROUPED>
 __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
-  constexpr int MT = kPreRows, CT = kPreChunks, RS = kPreRS;
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][MT * RS];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_i[2][CT * 4 * 16 * 4];
+  constexpr int MT = kPreRows, CT = kPreChunks;
+  constexpr int NDMA = GROUPED ? 8 : 7;  // DMA instructions per wave and k-step
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kPreLdsBytes];
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  const uint32_t lbase = (uint32_t)(size_t)(lds_u8*)lds;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // chunk pair of this wave
   const int M = a.M, N = a.N, K = a.K;
-  const int nks = K >> 6;
+  const int nks = K >> 6;  // even: the host requires K % 128 == 0
 
   // ---- tile order: each XCD (block b on XCD b % 8) works through a contiguous range
   // of tiles, in supertiles of GN column tiles x GM row tiles (rows fastest), so that
@@ -98,187 +126,262 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
     tn = t / ntm;
     tm = t % ntm;
   }
-  const int c0 = tn * CT;  // first chunk of the tile
-  const int m0 = tm * MT;  // first batch row
+  const int c0 = tn * CT;         // first chunk of the tile
+  const int m0 = tm * MT;         // first batch row
+  const int cw = c0 + 2 * w;      // first chunk of this wave
 
-  // ---- cooperative activation pieces: p = tid + 256q -> row p>>3, 16-byte piece p&7 ----
-  const _Float16* arow[4];
-  uint32_t aoff0[4], aoff1[4];
+  // ---- DMA sources: per-lane byte offsets from per-k-step bases ----
+  // activations: instruction u of wave w fills pieces 64(4w+u) + lane of the step's
+  // 1024 16-byte pieces; piece P = row P >> 3, physical slot P & 7, which holds the
+  // logical slot (P & 7) ^ ((row >> 1) & 7).  Rows past M repeat row M-1 (never
+  // stored); M*K < 2^31 is checked by the host.
+  uint32_t act_off[4];
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int p = tid + 256 * q, r = p >> 3, u = p & 7;
-    const int m = m0 + r < M ? m0 + r : M - 1;  // rows past M repeat row M-1 (never stored)
-    arow[q] = a.A + (size_t)m * K + 8 * u;
-    const int kb = u >> 2, g = 2 * (u & 3);
-    aoff0[q] = r * RS + 8 * pre_mgroup(kb, g);
-    aoff1[q] = r * RS + 8 * pre_mgroup(kb, g + 1);
+  for (int u = 0; u < 4; u++) {
+    const int p = 64 * (4 * w + u) + lane, row = p >> 3;
+    const int ls = (p & 7) ^ ((row >> 1) & 7);
+    const int m = m0 + row < M ? m0 + row : M - 1;
+    act_off[u] = ((uint32_t)m * (uint32_t)K + 8 * ls) * 2;
   }
-  // ---- cooperative metadata units: chunk tid>>5, unit tid&31 (both k-blocks) ----
-  const int mq = tid & 31, mcc = tid >> 5;
-  const uint8_t* mbase = static_cast<const uint8_t*>(a.meta) + 256 * (size_t)(c0 + mcc) + 8 * mq;
-  const size_t mrow = 4 * (size_t)N;  // bytes per k-block row of metadata
-  const int mj = 2 * (mq >> 4) + (mq & 1), mg8 = (mq >> 1) & 7;
-  const uint32_t ioff = (((mcc * 4 + mj) * 16 + 2 * mg8) * 4) * 2;  // byte offset of [rho=2g8][h=0]
+  // packed values of k-block kb: chunk cw + (lane >> 5), 16-byte piece lane & 31
+  const uint32_t wv_off = 512 * (uint32_t)(cw + (lane >> 5)) + 16 * (lane & 31);
+  const uint32_t wv_kb = 8 * (uint32_t)N;  // bytes per k-block row of values
+  // metadata: k-block lane >> 5, chunk cw + ((lane >> 4) & 1), piece lane & 15
+  const uint32_t mt_off = (lane >> 5) * 4 * (uint32_t)N + 256 * (uint32_t)(cw + ((lane >> 4) & 1)) + 16 * (lane & 15);
+  // scales (4 bytes per lane): chunk cw + (lane >> 5), dword lane & 31
+  const uint32_t sc_off = 128 * (uint32_t)(cw + (lane >> 5)) + 4 * (lane & 31);
+
+  const char* gA = reinterpret_cast<const char*>(a.A);
+  const char* gB = static_cast<const char*>(a.B);
+  const char* gM = static_cast<const char*>(a.meta);
+  const char* gS = reinterpret_cast<const char*>(a.s);
+
+  // DMA instruction i (0..NDMA-1) of k-step s (clamped to the last) into ring slot q
+  auto dma = [&](int s, int q, int i) {
+    const int sc = s < nks ? s : nks - 1;
+    if (i < 4) {
+      pre_dma16(lbase + kPreActOff + q * kPreActB + 1024 * (4 * w + i), act_off[i], gA + 128 * (size_t)sc);
+    } else if (i < 6) {
+      pre_dma16(lbase + kPreWOff + q * kPreWB + 2048 * w + 1024 * (i - 4), wv_off + (i - 4) * wv_kb,
+                gB + 16 * (size_t)sc * N);
+    } else if (i == 6) {
+      pre_dma16(lbase + kPreMOff + q * kPreMB + 1024 * w, mt_off, gM + 8 * (size_t)sc * N);
+    } else {
+      pre_dma4(lbase + kPreSOff + q * kPreSB + 256 * w, sc_off, gS + 2 * (size_t)(sc >> 1) * N);
+    }
+  };
 
   // ---- this lane's MFMA roles ----
-  const int rho = lane & 15, h = lane >> 4;
-  const int g8 = rho >> 1, blk = rho & 1;
-  const uint32_t vsh = 8u * blk;
-  // packed values of chunk cl, k-block kb of k-step s: 16 bytes (words j = 0..3)
-  const uint8_t* vbase = static_cast<const uint8_t*>(a.B) + 512 * (size_t)(c0 + 2 * wave) + 4 * (16 * g8 + 4 * h);
-  const size_t vrow = 8 * (size_t)N;  // bytes per k-block row of values
-  // scales of chunk cl: 16 bytes at slot 8*g8 (halves blk + 2f)
-  const uint8_t* sbase = reinterpret_cast<const uint8_t*>(a.s) + 2 * (64 * (size_t)(c0 + 2 * wave) + 8 * g8);
-  const size_t srow = 2 * (size_t)N;
-  const uint32_t bofs = (uint32_t)rho * RS + 16 * h;                   // B fragment bf: + 16*bf*RS
-  const uint32_t iofs = ((((2 * wave) * 4) * 16 + rho) * 4 + h) * 2;   // idx of chunk cl, fragment f: + (cl*4+f)*128
+  const int rho = lane & 31, h = lane >> 5;
+  const int g8 = rho >> 2, j = rho & 3;
+  const int swz = (rho >> 1) & 7;
+  // B fragment (kb, rg): row 32rg + rho, logical slots 4kb + 2h + {0, 1}
+  uint32_t b_off[2][2];
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+    for (int i = 0; i < 2; i++) b_off[kb][i] = kPreActOff + rho * 128 + 16 * ((4 * kb + 2 * h + i) ^ swz);
+  // packed words (kb, c, t = 2h) and (kb, c, 2h + 1) of column pair (8g8 + j, +4): + 16
+  const uint32_t w_rd = kPreWOff + 2048 * w + 4 * (16 * g8 + 8 * h + j);
+  // metadata unit of the column pair
+  const uint32_t m_rd = kPreMOff + 1024 * w + 8 * (16 * (j >> 1) + 2 * g8 + (j & 1));
+  // scales of columns 8g8 + j (+4): slots 8g8 + 2j, + 1
+  const uint32_t s_rd = kPreSOff + 256 * w + 16 * g8 + 4 * j;
+  // index halfwords of both halves: [d0.b(h), d1.b(h), d0.b(2+h), d1.b(2+h)]
+  const uint32_t isel = h ? 0x07030501u : 0x06020400u;
 
   uint32_t kMask, kMagic, kMaskHi;
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
   asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
 
-  auto clampk = [&](int s) { return s < nks ? s : nks - 1; };
-  u32x4 ast[4];          // activation staging (next k-step)
-  u32x2 mst0, mst1;      // metadata staging (k-blocks 0 and 1)
-  u32x4 vreg[2][2][2];   // [ring slot][chunk][k-block] packed values
-  u32x4 sreg[2][2];      // [ring slot][chunk] scales
-  auto load_stage = [&](int s) {
-    const int sc = clampk(s);
+  half8_t av[2][2][4];   // [parity][kb][2c + hf] dequantized weight fragments
+  uint32_t ix[2][2][2];  // [parity][kb][c] index halfwords (hf = abid)
+  half16_t bv[4];        // B fragments, ring by fragment number kb*4 + rg
+  f32x16 acc[4][4];      // [rg][2c + hf]
 #pragma unroll
-    for (int q = 0; q < 4; q++) ast[q] = *reinterpret_cast<const u32x4*>(arow[q] + 64 * sc);
-    mst0 = *reinterpret_cast<const u32x2*>(mbase + (size_t)(2 * sc) * mrow);
-    mst1 = *reinterpret_cast<const u32x2*>(mbase + (size_t)(2 * sc + 1) * mrow);
-  };
-  auto load_weights = [&](int s, int slot) {
-    const int sc = clampk(s);
+  for (int rg = 0; rg < 4; rg++)
 #pragma unroll
-    for (int cl = 0; cl < 2; cl++) {
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-        vreg[slot][cl][kb] = *reinterpret_cast<const u32x4*>(vbase + 512 * cl + (size_t)(2 * sc + kb) * vrow);
-      if constexpr (GROUPED)
-        sreg[slot][cl] = *reinterpret_cast<const u32x4*>(sbase + 128 * cl + (size_t)(sc >> 1) * srow);
+    for (int af = 0; af < 4; af++) {
+      acc[rg][af] = (f32x16){};
+      asm volatile("" : "+a"(acc[rg][af]));
     }
-  };
-  auto write_stage = [&](int buf) {
-    uint8_t* la = lds_a[buf];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      *reinterpret_cast<u32x2*>(la + aoff0[q]) = (u32x2){ast[q].x, ast[q].y};
-      *reinterpret_cast<u32x2*>(la + aoff1[q]) = (u32x2){ast[q].z, ast[q].w};
-    }
-    u32x2 lo, hi;
-    pre_meta_transpose(mst0.x, mst0.y, mst1.x, mst1.y, lo, hi);
-    *reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(lds_i[buf]) + ioff) = (u32x4){lo.x, lo.y, hi.x, hi.y};
+
+  auto read_b = [&](int q, int f) -> half16_t {
+    const int kb = f >> 2, rg = f & 3;
+    const uint8_t* p0 = lds + b_off[kb][0] + q * kPreActB + rg * 4096;
+    const uint8_t* p1 = lds + b_off[kb][1] + q * kPreActB + rg * 4096;
+    const half8_t lo = *reinterpret_cast<const half8_t*>(p0);
+    const half8_t hi = *reinterpret_cast<const half8_t*>(p1);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
   };
 
-  float4_t acc[2][4][8];
+  // raw operands of the next k-step's dequantization, combo k = (kb, c) = (k >> 1, k & 1)
+  uint32_t rw[4][2];  // packed words t = 2h, 2h + 1
+  u32x2 rm[4];        // metadata unit
+  uint32_t rs[2];     // scales of columns (8g8 + j, + 4), per chunk
+  auto read_raw = [&](int q, int k) {
+    const int kb = k >> 1, c = k & 1;
+    const uint8_t* pw = lds + w_rd + q * kPreWB + 1024 * kb + 512 * c;
+    rw[k][0] = *reinterpret_cast<const uint32_t*>(pw);
+    rw[k][1] = *reinterpret_cast<const uint32_t*>(pw + 16);
+    rm[k] = *reinterpret_cast<const u32x2*>(lds + m_rd + q * kPreMB + 512 * kb + 256 * c);
+  };
+  auto read_scales = [&](int q) {
+    if constexpr (GROUPED) {
 #pragma unroll
-  for (int cl = 0; cl < 2; cl++)
-#pragma unroll
-    for (int f = 0; f < 4; f++)
-#pragma unroll
-      for (int bf = 0; bf < 8; bf++) acc[cl][f][bf] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 2; c++) rs[c] = *reinterpret_cast<const uint32_t*>(lds + s_rd + q * kPreSB + 128 * c);
+    }
+  };
 
-  // buf / slot are compile-time (the k-loop is unrolled by two): a runtime ring index
-  // would turn every register access into indexed moves with full waits.  The eight
-  // weight fragments are dequantized first (32 registers); the activation fragments
-  // are then streamed from LDS, each used by all eight.
-  auto compute = [&](auto par) {
-    constexpr int buf = decltype(par)::value, slot = buf;
-    const uint8_t* la = lds_a[buf];
-    const uint8_t* li = reinterpret_cast<const uint8_t*>(lds_i[buf]);
-    uint32_t idxs[2][4];
-#pragma unroll
-    for (int cl = 0; cl < 2; cl++)
-#pragma unroll
-      for (int f = 0; f < 4; f++) idxs[cl][f] = *reinterpret_cast<const uint16_t*>(li + iofs + (cl * 4 + f) * 128);
-    half8_t av[2][4];
-#pragma unroll
-    for (int cl = 0; cl < 2; cl++) {
-#pragma unroll
-      for (int f = 0; f < 4; f++) {
-        const uint32_t w0 = vreg[slot][cl][0][f] >> vsh;
-        const uint32_t w1 = vreg[slot][cl][1][f] >> vsh;
-        const half2_t p0 = __builtin_bit_cast(half2_t, (w0 & kMask) | kMagic) - (half2_t){(_Float16)1032.f, (_Float16)1032.f};
-        const half2_t p1 = __builtin_bit_cast(half2_t, (w0 & kMaskHi) | kMagic) * (half2_t){(_Float16)0.0625f, (_Float16)0.0625f} +
-                           (half2_t){(_Float16)-72.f, (_Float16)-72.f};
-        const half2_t p2 = __builtin_bit_cast(half2_t, (w1 & kMask) | kMagic) - (half2_t){(_Float16)1032.f, (_Float16)1032.f};
-        const half2_t p3 = __builtin_bit_cast(half2_t, (w1 & kMaskHi) | kMagic) * (half2_t){(_Float16)0.0625f, (_Float16)0.0625f} +
-                           (half2_t){(_Float16)-72.f, (_Float16)-72.f};
-        av[cl][f] = (half8_t){p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-        if constexpr (GROUPED) {
-          const uint32_t sw = sreg[slot][cl][f] >> (16 * blk);
-          const _Float16 sc = __builtin_bit_cast(half2_t, sw).x;
-          av[cl][f] = av[cl][f] * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
-        }
+  // ---- dequantization of combo k into av[par][kb][2c + hf], ix[par][kb][c], in seven
+  // slices of at most four VALU instructions: word halves -> magic-number halves
+  // 1024 + q (low nibbles) or 1024 + 16q (high nibbles) -> q - 8 -> times scale ----
+  uint32_t dx[2][4];
+  half2_t dp[2][4];
+  auto dq_slice = [&](int k, int sl, int par) {
+    const int kb = k >> 1, c = k & 1;
+    const half2_t k1032 = {(_Float16)1032.f, (_Float16)1032.f};
+    const half2_t k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2_t km72 = {(_Float16)-72.f, (_Float16)-72.f};
+    const uint32_t w0 = rw[k][0], w1 = rw[k][1];
+    const half2_t scv = __builtin_bit_cast(half2_t, rs[c]);
+    auto scl = [&](int hf, int i) {
+      if constexpr (GROUPED) {
+        const _Float16 sv = hf ? scv.y : scv.x;
+        dp[hf][i] = dp[hf][i] * (half2_t){sv, sv};
       }
-    }
+    };
+    switch (sl) {
+      case 0:
+        dx[1][0] = w0 >> 8;  // (shifted words, turned into halves in the next slice)
+        dx[1][1] = w1 >> 8;
+        dx[0][0] = (w0 & kMask) | kMagic;
+        dx[0][1] = (w1 & kMask) | kMagic;
+        break;
+      case 1:
+        dx[0][2] = (w0 & kMaskHi) | kMagic;
+        dx[0][3] = (w1 & kMaskHi) | kMagic;
+        dx[1][2] = (dx[1][0] & kMaskHi) | kMagic;
+        dx[1][3] = (dx[1][1] & kMaskHi) | kMagic;
+        break;
+      case 2:
+        dx[1][0] = (dx[1][0] & kMask) | kMagic;
+        dx[1][1] = (dx[1][1] & kMask) | kMagic;
+        dp[0][0] = __builtin_bit_cast(half2_t, dx[0][0]) - k1032;
+        dp[0][1] = __builtin_bit_cast(half2_t, dx[0][1]) - k1032;
+        break;
+      case 3:
+        dp[0][2] = __builtin_bit_cast(half2_t, dx[0][2]) * k16th + km72;
+        dp[0][3] = __builtin_bit_cast(half2_t, dx[0][3]) * k16th + km72;
+        dp[1][0] = __builtin_bit_cast(half2_t, dx[1][0]) - k1032;
+        dp[1][1] = __builtin_bit_cast(half2_t, dx[1][1]) - k1032;
+        break;
+      case 4:
+        dp[1][2] = __builtin_bit_cast(half2_t, dx[1][2]) * k16th + km72;
+        dp[1][3] = __builtin_bit_cast(half2_t, dx[1][3]) * k16th + km72;
+        scl(0, 0);
+        scl(0, 1);
+        break;
+      case 5:
+        scl(0, 2);
+        scl(0, 3);
+        scl(1, 0);
+        scl(1, 1);
+        break;
+      default:
+        scl(1, 2);
+        scl(1, 3);
+        ix[par][kb][c] = __builtin_amdgcn_perm(rm[k].y, rm[k].x, isel);
 #pragma unroll
-    for (int bf = 0; bf < 8; bf++) {
-      const half8_t lo = *reinterpret_cast<const half8_t*>(la + bofs + 16 * bf * RS);
-      const half8_t hi = *reinterpret_cast<const half8_t*>(la + bofs + 16 * bf * RS + 64);
-      const half16_t bv = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-#pragma unroll
-      for (int cl = 0; cl < 2; cl++)
-#pragma unroll
-        for (int f = 0; f < 4; f++) acc[cl][f][bf] = smfmac64<0>(av[cl][f], bv, acc[cl][f][bf], idxs[cl][f]);
+        for (int hf = 0; hf < 2; hf++)
+          av[par][kb][2 * c + hf] = (half8_t){dp[hf][0].x, dp[hf][0].y, dp[hf][1].x, dp[hf][1].y,
+                                              dp[hf][2].x, dp[hf][2].y, dp[hf][3].x, dp[hf][3].y};
+        break;
     }
   };
 
-  // ---- pipeline: k-step s computes from LDS buffer / weight slot s & 1 while the
-  // activations and metadata of s+1 are written to the other buffer and those of s+2
-  // and the weights of s+2 are loaded.  Loads are unconditional (clamped to the last
-  // k-step), so the compiler's waits stay exact; the loop is unrolled by two. ----
-  auto step = [&](int s, auto par) {
-    constexpr int P = decltype(par)::value;
-    __syncthreads();
-    if (s + 1 < nks) write_stage(P ^ 1);  // uniform
-    load_stage(s + 2);
-    if (s < nks) compute(par);            // uniform: false only after an odd k-step count
-    load_weights(s + 2, P);
+  // ---- k-step s in ring slot Q = s & 3 (slot Q+1: step s+1, slot Q+3: step s+3):
+  //   barrier: this wave's DMAs of step s+1 have landed, every wave has finished step
+  //   s-1 (its reads of slot Q+3);
+  //   32 regions r = (kb, rg, c, hf), each one MFMA plus a share of: the DMAs of step
+  //   s+3 (r < NDMA); at hf = c = 0 the read of B fragment f+2 (f = 4kb + rg; from
+  //   step s+1 past 7); at r < 4 the raw words and metadata of step s+1, combo r, and
+  //   at r = 4 its scales; at r >= 4 slice (r-4) % 7 of dequantizing combo (r-4) / 7
+  //   of step s+1.
+  // Steps past the last are skipped (uniform); the DMAs are clamped, so the vmcnt of
+  // every barrier counts exactly the DMAs of one step. ----
+  auto step = [&](int s, auto qc) {
+    constexpr int Q = decltype(qc)::value, P = Q & 1, QN = (Q + 1) & 3, QD = (Q + 3) & 3;
+    pre_step_barrier<NDMA>();
+#pragma unroll
+    for (int r = 0; r < 32; r++) {
+      const int kb = r >> 4, rg = (r >> 2) & 3, af = r & 3, c = af >> 1, hf = af & 1, f = r >> 2;
+      if (hf) pre_smfmac<1>(acc[rg][af], av[P][kb][af], bv[f & 3], ix[P][kb][c]);
+      else pre_smfmac<0>(acc[rg][af], av[P][kb][af], bv[f & 3], ix[P][kb][c]);
+      __builtin_amdgcn_sched_barrier(0);  // the region's work follows its MFMA
+      if (af == 0) bv[(f + 2) & 3] = read_b(f + 2 < 8 ? Q : QN, (f + 2) & 7);
+      if (r < NDMA) dma(s + 3, QD, r);
+      if (r < 4) read_raw(QN, r);
+      if (r == 4) read_scales(QN);
+      if (r >= 4) dq_slice((r - 4) / 7, (r - 4) % 7, P ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  load_stage(0);
-  load_weights(0, 0);
-  load_weights(1, 1);
-  write_stage(0);
-  load_stage(1);
-  for (int s = 0; s < nks; s += 2) {
+
+  // ---- prologue: DMAs of steps 0..2, then step 0's operands dequantized and its first
+  // two B fragments read ----
+#pragma unroll
+  for (int s = 0; s < 3; s++)
+#pragma unroll
+    for (int i = 0; i < NDMA; i++) dma(s, s, i);
+  pre_step_barrier<NDMA>();
+#pragma unroll
+  for (int k = 0; k < 4; k++) read_raw(0, k);
+  read_scales(0);
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+#pragma unroll
+    for (int sl = 0; sl < 7; sl++) dq_slice(k, sl, 0);
+  bv[0] = read_b(0, 0);
+  bv[1] = read_b(0, 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  for (int s = 0; s < nks; s += 4) {
     step(s, IntC<0>{});
-    step(s + 1, IntC<1>{});
-  }
-
-  // ---- epilogue: lane (mcol = rho, h) holds rows 4h+i of every fragment, i.e. for
-  // chunk cl and batch block bf the 16 columns 64c + 16h + [0, 16) (f fastest) of
-  // batch row m0 + 16*bf + rho ----
-#pragma unroll
-  for (int cl = 0; cl < 2; cl++) {
-    const int n = 64 * (c0 + 2 * wave + cl) + 16 * h;
-    half8_t sc0 = {}, sc1 = {};
-    if constexpr (!GROUPED) {
-      sc0 = *reinterpret_cast<const half8_t*>(a.s + n);
-      sc1 = *reinterpret_cast<const half8_t*>(a.s + n + 8);
+    step(s + 1, IntC<1>{});  // nks is even
+    if (s + 2 < nks) {
+      step(s + 2, IntC<2>{});
+      step(s + 3, IntC<3>{});
     }
+  }
+  // DMAs of (clamped) steps past the last may still be landing in LDS
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  pre_mfma_drain();
 #pragma unroll
-    for (int bf = 0; bf < 8; bf++) {
-      const int m = m0 + 16 * bf + rho;
-      half8_t o0, o1;
+  for (int rg = 0; rg < 4; rg++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
+    for (int af = 0; af < 4; af++) asm volatile("" : "+a"(acc[rg][af]));
+
+  // ---- epilogue: lane (rho, h) holds, for batch row m0 + 32rg + rho, the columns
+  // 64c' + 16q + 8h + 4hf + i (c' = cw + c) in register 4q + i of acc[rg][2c + hf]:
+  // eight consecutive columns per (rg, c, q) ----
 #pragma unroll
-        for (int f = 0; f < 4; f++) {
-          const int e = 4 * i + f;  // column n + e
-          _Float16 v = (_Float16)acc[cl][f][bf][i];
-          if constexpr (!GROUPED) v = v * (e < 8 ? sc0[e & 7] : sc1[e & 7]);
-          if (e < 8) o0[e] = v;
-          else o1[e - 8] = v;
+  for (int rg = 0; rg < 4; rg++) {
+    const int m = m0 + 32 * rg + rho;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int n = 64 * (cw + c) + 16 * q + 8 * h;
+        half8_t o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          o[i] = (_Float16)acc[rg][2 * c][4 * q + i];
+          o[4 + i] = (_Float16)acc[rg][2 * c + 1][4 * q + i];
         }
-      }
-      if (m < M) {
-        _Float16* cp = a.C + (size_t)m * N + n;
-        *reinterpret_cast<half8_t*>(cp) = o0;
-        *reinterpret_cast<half8_t*>(cp + 8) = o1;
+        if constexpr (!GROUPED) o = o * *reinterpret_cast<const half8_t*>(a.s + n);
+        if (m < M) *reinterpret_cast<half8_t*>(a.C + (size_t)m * N + n) = o;
       }
     }
   }

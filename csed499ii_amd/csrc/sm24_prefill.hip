@@ -1,5 +1,4 @@
-// Large-M 2:4 INT4 x FP16 GEMM: instantiation and launch of sm24_prefill_kernel
-// (compiled on its own, with the MFMA register-form flag of build.py).
+// Large-M 2:4 INT4 x FP16 GEMM: instantiation and launch of sm24_prefill_kernel.
 #include "sm24_prefill.h"
 
 namespace sm24 {
