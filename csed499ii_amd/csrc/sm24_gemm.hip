@@ -363,6 +363,35 @@ int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** co
   return MARLIN_HIP_OK;
 }
 
+// K splits of the large-M kernel.  Its workgroups fill the CUs one per CU, so a
+// problem with few tiles runs faster split along K when K is long enough to pay for
+// the hand-off: each split stores a 256 KiB fp32 partial to uncached scratch and the
+// last one reads them all back.  The estimate is rounds x (k-steps per split) plus
+// that traffic, at the rates measured on MI355X (0.67 us per k-step of a tile, ~1.4
+// TB/s for the exchange).  MARLIN_HIP_PREFILL_SPLITS forces a count (read once).
+int prefill_splits(int tiles, int nks, int cus) {
+  static const int forced = [] {
+    const char* e = getenv("MARLIN_HIP_PREFILL_SPLITS");
+    const int x = e ? atoi(e) : 0;
+    return x >= 1 && x <= 16 ? x : 0;
+  }();
+  const int max_s = nks / 8;  // at least eight k-steps per split
+  if (forced) return forced < max_s ? forced : (max_s > 0 ? max_s : 1);
+  const double step_us = 0.67, exchange_bytes_per_us = 1.4e6;
+  int best_s = 1;
+  double best = 1e30;
+  for (int s = 1; s <= 8 && s <= max_s; s++) {
+    const long long rounds = ((long long)tiles * s + cus - 1) / cus;
+    const double traffic = s > 1 ? 2.0 * tiles * s * (double)kPreSplitBytes : 0.0;
+    const double cost = (double)rounds * step_us * nks / s + traffic / exchange_bytes_per_us;
+    if (cost < 0.97 * best) {
+      best = cost;
+      best_s = s;
+    }
+  }
+  return best_s;
+}
+
 struct Plan {
   int bb;
   int splits;
@@ -585,7 +614,16 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
     p.M = M;
     p.N = N;
     p.K = K;
-    p.splits = 1;
+    const int tiles = (N / kPreTileCols) * ((M + 127) / 128);
+    p.splits = prefill_splits(tiles, K / 64, sms);
+    if (p.splits > 1 && (size_t)tiles * sizeof(uint32_t) > kCounterBytes) p.splits = 1;
+    if (p.splits > 1) {
+      err = get_scratch(dev, stream, (size_t)tiles * p.splits * kPreSplitBytes, &p.counters, &p.partial);
+      if (err != MARLIN_HIP_OK) {
+        if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+        return err;
+      }
+    }
     hipError_t e = launch_prefill(p, groupsize != -1, stream);
     if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
     if (e != hipSuccess) {

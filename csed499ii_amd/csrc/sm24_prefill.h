@@ -107,12 +107,20 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   const int M = a.M, N = a.N, K = a.K;
   const int nks = K >> 6;  // even: the host requires K % 128 == 0
 
+  // ---- split-K: block b = z * T + tile; split z covers the k-steps [ks0, ks1), an even
+  // number (>= 8: the host keeps splits <= nks / 8) ----
+  const int ntn = N / (64 * CT), ntm = (M + MT - 1) / MT;
+  const int T = ntn * ntm;
+  const int S = a.splits;
+  const int z = blockIdx.x / T;
+  const int ks0 = 2 * (int)(((long long)(nks >> 1) * z) / S);
+  const int ks1 = 2 * (int)(((long long)(nks >> 1) * (z + 1)) / S);
+
   // ---- tile order: each XCD (block b on XCD b % 8) works through a contiguous range
   // of tiles, in supertiles of GN column tiles x GM row tiles (rows fastest), so that
   // the workgroups resident on one XCD share weights and activations in its L2. ----
-  const int ntn = N / (64 * CT), ntm = (M + MT - 1) / MT;
-  const int T = ntn * ntm;
-  int t = blockIdx.x;
+  const int tile = blockIdx.x - z * T;
+  int t = tile;
   if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
   const int GM = ntm >= 8 ? 8 : ntm;
   const int GN = 32 / GM;
@@ -156,9 +164,10 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   const char* gM = static_cast<const char*>(a.meta);
   const char* gS = reinterpret_cast<const char*>(a.s);
 
-  // DMA instruction i (0..NDMA-1) of k-step s (clamped to the last) into ring slot q
+  // DMA instruction i (0..NDMA-1) of local k-step s (clamped to the split's last) into
+  // ring slot q
   auto dma = [&](int s, int q, int i) {
-    const int sc = s < nks ? s : nks - 1;
+    const int sc = ks0 + s < ks1 ? ks0 + s : ks1 - 1;
     if (i < 4) {
       pre_dma16(lbase + kPreActOff + q * kPreActB + 1024 * (4 * w + i), act_off[i], gA + 128 * (size_t)sc);
     } else if (i < 6) {
@@ -347,10 +356,11 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   bv[1] = read_b(0, 1);
   __builtin_amdgcn_sched_barrier(0);
 
-  for (int s = 0; s < nks; s += 4) {
+  const int nls = ks1 - ks0;  // k-steps of this split (even)
+  for (int s = 0; s < nls; s += 4) {
     step(s, IntC<0>{});
-    step(s + 1, IntC<1>{});  // nks is even
-    if (s + 2 < nks) {
+    step(s + 1, IntC<1>{});
+    if (s + 2 < nls) {
       step(s + 2, IntC<2>{});
       step(s + 3, IntC<3>{});
     }
@@ -363,6 +373,43 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
 #pragma unroll
     for (int af = 0; af < 4; af++) asm volatile("" : "+a"(acc[rg][af]));
 
+  // ---- split-K hand-off: the partial tile goes to uncached scratch in register order
+  // ([tile][split][wave][rg][2c+hf][i][lane] float4s, 256 KiB per tile and split); the
+  // last split to arrive at the tile's counter reads all splits back and adds them in
+  // split order (so the result is bit-identical from run to run, whichever split comes
+  // last), writes C and resets the counter.  Each thread's stores complete before the
+  // workgroup barrier; the counter is bumped after it. ----
+  const float* const pbase = a.partial + ((size_t)tile * S) * 65536 + (size_t)w * 16384 + 4 * lane;
+  if (S > 1) {
+    float* const pmine = a.partial + ((size_t)tile * S + z) * 65536 + (size_t)w * 16384 + 4 * lane;
+#pragma unroll
+    for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+      for (int af = 0; af < 4; af++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          *reinterpret_cast<float4_t*>(pmine + ((rg * 4 + af) * 4 + i) * 256) =
+              (float4_t){acc[rg][af][4 * i], acc[rg][af][4 * i + 1], acc[rg][af][4 * i + 2], acc[rg][af][4 * i + 3]};
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    __shared__ uint32_t arrived;
+    if (tid == 0) arrived = __hip_atomic_fetch_add(a.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    __syncthreads();
+    if (arrived != (uint32_t)S) return;
+    if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // accumulator float4 (rg, af, i) of this lane: registers, or the sum of the splits
+  auto result = [&](int rg, int af, int i) -> float4_t {
+    if (S == 1)
+      return (float4_t){acc[rg][af][4 * i], acc[rg][af][4 * i + 1], acc[rg][af][4 * i + 2], acc[rg][af][4 * i + 3]};
+    float4_t v = {0.f, 0.f, 0.f, 0.f};
+    const float* p = pbase + ((rg * 4 + af) * 4 + i) * 256;
+    for (int zz = 0; zz < S; zz++) v += *reinterpret_cast<const float4_t*>(p + (size_t)zz * 65536);
+    return v;
+  };
+
   // ---- epilogue: lane (rho, h) holds, for batch row m0 + 32rg + rho, the columns
   // 64c' + 16q + 8h + 4hf + i (c' = cw + c) in register 4q + i of acc[rg][2c + hf]:
   // eight consecutive columns per (rg, c, q) ----
@@ -374,12 +421,9 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const int n = 64 * (cw + c) + 16 * q + 8 * h;
-        half8_t o;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          o[i] = (_Float16)acc[rg][2 * c][4 * q + i];
-          o[4 + i] = (_Float16)acc[rg][2 * c + 1][4 * q + i];
-        }
+        const float4_t v0 = result(rg, 2 * c, q), v1 = result(rg, 2 * c + 1, q);
+        half8_t o = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+                     (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
         if constexpr (!GROUPED) o = o * *reinterpret_cast<const half8_t*>(a.s + n);
         if (m < M) *reinterpret_cast<half8_t*>(a.C + (size_t)m * N + n) = o;
       }

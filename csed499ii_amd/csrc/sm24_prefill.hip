@@ -4,7 +4,7 @@
 namespace sm24 {
 
 hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream) {
-  const int tiles = (a.N / (64 * kPreChunks)) * ((a.M + kPreRows - 1) / kPreRows);
+  const int tiles = (a.N / (64 * kPreChunks)) * ((a.M + kPreRows - 1) / kPreRows) * a.splits;
   if (grouped) hipLaunchKernelGGL(sm24_prefill_kernel<true>, dim3(tiles), dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(sm24_prefill_kernel<false>, dim3(tiles), dim3(256), 0, stream, a);
   return hipGetLastError();

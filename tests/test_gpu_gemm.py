@@ -142,6 +142,18 @@ def test_prefill_kernel_shapes(M, N, K, g):
     assert torch.equal(_run(wt, A), C), "repeated calls differ"
 
 
+@pytest.mark.parametrize("M,N,K,g", [(300, 512, 8192, -1), (1000, 2048, 8192, 128), (256, 1024, 4096, 128)])
+def test_prefill_split_k(M, N, K, g):
+    """Large-M kernel split along K (few tiles, long K: the planner picks 3-7 splits):
+    partials handed off through the scratch, reduced by the last split in split order,
+    so repeated calls agree bit for bit and the counters return to zero."""
+    wt, A = _problem(M, N, K, g, 1700 + M + K)
+    C = _run(wt, A)
+    _check(wt, A, C, f"prefill split-K M={M} N={N} K={K} g={g}")
+    for _ in range(3):
+        assert torch.equal(_run(wt, A), C), "repeated split-K calls differ"
+
+
 @pytest.mark.parametrize("M", [512])
 def test_prefill_shape_slices(M):
     wt, A = _problem(M, 8192, 8192, 128, 31)
