@@ -129,4 +129,22 @@ __device__ __forceinline__ float4_t smfmac64(half8_t a, half16_t b, float4_t c, 
   return __builtin_amdgcn_smfmac_f32_16x16x64_f16(a, b, c, (int)idx, 0, ABID);
 }
 
+// LDS-DMA: every lane copies 16 (4) bytes from base + voff to LDS byte address
+// lds + 16 (4) * lane.  Tracked by vmcnt, like any global load; `lds` must be
+// wave-uniform.  M0 is set here (one wait state before the DMA reads it).
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
+// Waits until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 }  // namespace sm24

@@ -75,17 +75,6 @@ __device__ __forceinline__ void pre_smfmac(f32x16& c, half8_t a, half16_t b, uin
 // Wait states between the last MFMA and the first read of its result.
 __device__ __forceinline__ void pre_mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 
-// LDS-DMA: every lane copies 16 (4) bytes from base + voff to LDS byte address
-// lds + 16 (4) * lane.  Tracked by vmcnt, like any global load.
-__device__ __forceinline__ void pre_dma16(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void pre_dma4(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
-}
-
 // Start of a k-step: this wave's DMAs except the last NDMA issued have landed, its
 // LDS reads are complete; then the workgroup meets.
 template <int NDMA>
@@ -169,14 +158,14 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   auto dma = [&](int s, int q, int i) {
     const int sc = ks0 + s < ks1 ? ks0 + s : ks1 - 1;
     if (i < 4) {
-      pre_dma16(lbase + kPreActOff + q * kPreActB + 1024 * (4 * w + i), act_off[i], gA + 128 * (size_t)sc);
+      dma16(lbase + kPreActOff + q * kPreActB + 1024 * (4 * w + i), act_off[i], gA + 128 * (size_t)sc);
     } else if (i < 6) {
-      pre_dma16(lbase + kPreWOff + q * kPreWB + 2048 * w + 1024 * (i - 4), wv_off + (i - 4) * wv_kb,
+      dma16(lbase + kPreWOff + q * kPreWB + 2048 * w + 1024 * (i - 4), wv_off + (i - 4) * wv_kb,
                 gB + 16 * (size_t)sc * N);
     } else if (i == 6) {
-      pre_dma16(lbase + kPreMOff + q * kPreMB + 1024 * w, mt_off, gM + 8 * (size_t)sc * N);
+      dma16(lbase + kPreMOff + q * kPreMB + 1024 * w, mt_off, gM + 8 * (size_t)sc * N);
     } else {
-      pre_dma4(lbase + kPreSOff + q * kPreSB + 256 * w, sc_off, gS + 2 * (size_t)(sc >> 1) * N);
+      dma4(lbase + kPreSOff + q * kPreSB + 256 * w, sc_off, gS + 2 * (size_t)(sc >> 1) * N);
     }
   };
 
