@@ -90,6 +90,17 @@ class Call:
         return 2 * self.M * self.K * self.N
 
 
+def kernel_of(c) -> str:
+    """The kernel the library dispatches a call to (the host rules of
+    csed499ii_amd/csrc/sm24_gemm.hip: decode for M <= 16, the prefill kernel for
+    M >= 256 with 4-bit values and metadata, N % 512 == 0 and K % 128 == 0)."""
+    if c.M <= 16:
+        return "sm24::sm24_decode_kernel"
+    if c.M >= 256 and c.bits == 4 and c.meta_key == "meta" and c.N % 512 == 0 and c.K % 128 == 0:
+        return "sm24::sm24_prefill_kernel"
+    return "sm24::sm24_gemm_kernel"
+
+
 def make_copies(K, N, seed, bits, copies, device, meta3=False) -> WeightSet:
     base = synth.make_weight(K, N, seed, 128, bits=bits, device=device)
     if meta3:
@@ -336,10 +347,8 @@ def main():
                 "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": None}
     if args.workload == "copy":
         roof["kernel"] = "device copy (calibration)"
-    elif max(c.M for c in calls) <= 16:
-        roof["kernel"] = "sm24::sm24_decode_kernel"
     else:
-        roof["kernel"] = "sm24::sm24_gemm_kernel" if min(c.M for c in calls) > 16 else "sm24 decode + gemm kernels"
+        roof["kernel"] = " + ".join(sorted({kernel_of(c) for c in calls}))
     roof["avg_launch_us"] = round(avg_launch_us, 3)
     roof["algorithmic_bytes_per_launch"] = round(step_bytes / len(calls))
     roof["traffic"] = traffic_from_profile(cfg["workload"])

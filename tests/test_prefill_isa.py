@@ -1,0 +1,154 @@
+"""ISA checks of the large-M kernel (CPU; needs hipcc, no GPU).
+
+sm24_prefill_kernel issues its MFMAs as inline assembly (accumulators in AGPRs), so
+the compiler's hazard recognizer does not guard them.  These tests compile the
+kernel to gfx950 assembly and check, on every instantiation, the two rules the
+kernel relies on (the wait states hipcc itself inserts around the v_smfmac builtin):
+
+* a VALU write of a register that an smfmac reads (A, B, index or accumulator)
+  lies at least 2 wait states before it;
+* nothing reads an smfmac's accumulator within 8 wait states after it, except a
+  following smfmac on the same accumulator (hardware-forwarded).
+
+A planted violation is caught (test_checker_catches_planted_hazards), so a pass
+means something.  They also check that the accumulators live in AGPRs and nothing
+spills.
+"""
+import os
+import pathlib
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+SRC = ROOT / "csed499ii_amd" / "csrc" / "sm24_prefill.hip"
+
+
+def _regs(tok):
+    m = re.match(r"^([va])\[(\d+):(\d+)\]$", tok)
+    if m:
+        return {(m.group(1), i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r"^([va])(\d+)$", tok)
+    return {(m.group(1), int(m.group(2)))} if m else set()
+
+
+def _instructions(body):
+    out = []
+    for line in body.split("\n"):
+        s = line.split(";")[0].strip()
+        if not s or s.startswith(".") or s.endswith(":"):
+            continue
+        parts = s.split(None, 1)
+        ops = [o.strip().split()[0] for o in parts[1].split(",") if o.strip()] if len(parts) > 1 else []
+        out.append((parts[0], s, ops))
+    return out
+
+
+def _wait_states(op, ops):
+    return int(ops[0], 0) + 1 if op == "s_nop" else 1
+
+
+def hazards(body):
+    """Violations of the two rules in one kernel's instruction stream (linear order,
+    plus the loop tail before a loop head)."""
+    ins = _instructions(body)
+    labels = {}
+    flat = []
+    for line in body.split("\n"):
+        s = line.split(";")[0].strip()
+        if s.endswith(":") and not s.startswith("."):
+            labels[s[:-1]] = len(flat)
+        elif s and not s.startswith("."):
+            parts = s.split(None, 1)
+            ops = [o.strip().split()[0] for o in parts[1].split(",") if o.strip()] if len(parts) > 1 else []
+            flat.append((parts[0], s, ops))
+    assert len(flat) == len(ins)
+    tails = {}
+    for k, (op, _, ops) in enumerate(flat):
+        if (op.startswith("s_cbranch") or op == "s_branch") and ops and ops[0] in labels and labels[ops[0]] <= k:
+            tails[labels[ops[0]]] = k
+    found = []
+    for i, (op, s, ops) in enumerate(flat):
+        if not op.startswith("v_smfmac"):
+            continue
+        reads = set().union(*(_regs(o) for o in ops[:4]))
+        window, w, j = [], 0, i - 1
+        while j >= 0 and w < 2:
+            window.append((flat[j], w))
+            w += _wait_states(flat[j][0], flat[j][2])
+            j -= 1
+        if i in tails:
+            w, j = 0, tails[i]
+            while j > i and w < 2:
+                window.append((flat[j], w))
+                w += _wait_states(flat[j][0], flat[j][2])
+                j -= 1
+        for (pop, ps, pops), pw in window:
+            if pop.startswith("v_") and not pop.startswith("v_smfmac") and pops and _regs(pops[0]) & reads:
+                found.append(f"VALU write {pw} wait states before smfmac: {ps!r} -> {s!r}")
+        dst, w, j = _regs(ops[0]), 0, i + 1
+        while j < len(flat) and w < 8:
+            nop, ns, nops = flat[j]
+            if nop.startswith("v_smfmac") and _regs(nops[0]) == dst:
+                break
+            if nop.startswith(("global_store", "buffer_store", "flat_store", "ds_write")):
+                rd = set().union(*(_regs(o) for o in nops)) if nops else set()
+            else:
+                rd = set().union(*(_regs(o) for o in nops[1:])) if nops else set()
+            if rd & dst:
+                found.append(f"accumulator read {w} wait states after smfmac: {s!r} -> {ns!r}")
+            w += _wait_states(nop, nops)
+            j += 1
+    return found
+
+
+def _kernels(asm):
+    return {m.group(1): m.group(0) for m in re.finditer(r"\n(_Z\w*sm24_prefill_kernel\w*):.*?s_endpgm", asm, re.S)}
+
+
+@pytest.fixture(scope="module")
+def prefill_asm(tmp_path_factory):
+    hipcc = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not pathlib.Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa") / "prefill.s"
+    from csed499ii_amd import build
+    cmd = [hipcc, *build.compile_flags(), *build.EXTRA_FLAGS.get(SRC.name, []), "--cuda-device-only", "-S",
+           "-o", str(out), str(SRC)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    return out.read_text()
+
+
+def test_checker_catches_planted_hazards():
+    planted = """
+\tv_pk_mul_f16 v9, v1, v2
+\ts_nop 0
+\tv_smfmac_f32_32x32x32_f16 a[0:15], v[8:11], v[20:27], v30
+\tv_accvgpr_read_b32 v0, a1
+\tv_mov_b32_e32 v30, 0
+\ts_nop 1
+\tv_smfmac_f32_32x32x32_f16 a[16:31], v[8:11], v[20:27], v30
+\ts_nop 7
+\tglobal_store_dwordx4 v0, a[16:19], s[0:1]
+"""
+    found = hazards(planted)
+    assert len(found) == 2, found
+    assert "1 wait states before" in found[0] and "accumulator read 0" in found[1]
+
+
+def test_prefill_smfmac_hazards(prefill_asm):
+    kernels = _kernels(prefill_asm)
+    assert len(kernels) == 2  # grouped and per-column scales
+    for name, body in kernels.items():
+        assert sum(1 for l in body.split("\n") if "v_smfmac" in l) >= 128, name
+        assert hazards(body) == [], name
+
+
+def test_prefill_registers(prefill_asm):
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", prefill_asm, re.S):
+        body = m.group(2)
+        assert int(re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", body).group(1)) == 0, m.group(1)
+    # 256 accumulator registers in AGPRs, no VGPR<->AGPR copies in the k-loop
+    assert prefill_asm.count("; NumAgprs: 256") == 2
