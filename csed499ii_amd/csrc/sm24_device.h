@@ -141,6 +141,45 @@ __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* ba
                : "memory", "m0");
 }
 
+// Four LDS-DMAs of 16 bytes per lane into lds + 1024 u + 16 lane (u = 0..3) from
+// base + v[u] + 1024 u: one M0 value, instruction offsets 0/1024/2048/3072 (applied to
+// both addresses).
+__device__ __forceinline__ void dma16x4(uint32_t lds, const uint32_t (&v)[4], const void* base) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %5\n\t"
+      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:3072" ::"s"(lds),
+      "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "s"(base)
+      : "memory", "m0");
+}
+// The weight side of a k-step for one wave, into lds + [0, 3328): 16 bytes per lane
+// from bw + v0 (-> lds), bw + v1 + 1024 (-> + 1024) and bm + vm + 2048 (-> + 2048),
+// then 4 bytes per lane from bs + vs + 3072 (-> + 3072).
+__device__ __forceinline__ void dma_weights(uint32_t lds, uint32_t v0, uint32_t v1, const void* bw, uint32_t vm,
+                                            const void* bm, uint32_t vs, const void* bs) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %3\n\t"
+      "global_load_lds_dwordx4 %2, %3 offset:1024\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:2048\n\t"
+      "global_load_lds_dword %6, %7 offset:3072" ::"s"(lds),
+      "v"(v0), "v"(v1), "s"(bw), "v"(vm), "s"(bm), "v"(vs), "s"(bs)
+      : "memory", "m0");
+}
+// As dma_weights without the scales.
+__device__ __forceinline__ void dma_weights_nos(uint32_t lds, uint32_t v0, uint32_t v1, const void* bw, uint32_t vm,
+                                                const void* bm) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %3\n\t"
+      "global_load_lds_dwordx4 %2, %3 offset:1024\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:2048" ::"s"(lds),
+      "v"(v0), "v"(v1), "s"(bw), "v"(vm), "s"(bm)
+      : "memory", "m0");
+}
+
 // Waits until at most N vector-memory operations of this wave are in flight.
 template <int N>
 __device__ __forceinline__ void wait_vm() {

@@ -527,7 +527,7 @@ bool prefill_fits(int M, int N, int K, int vf, int mf) {
     return x > 16 ? x : 256;
   }();
   return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 128 == 0 &&
-         (long long)M * K < (1LL << 31);
+         (long long)M * K < (1LL << 31) - 2048 && (long long)K * N < (1LL << 34);
 }
 
 // Shape/tile validation with the reference's rules and error codes

@@ -47,14 +47,15 @@ constexpr int kPreChunks = 8;  // 64-column chunks per tile
 static_assert(64 * kPreChunks == kPreTileCols, "tile width");
 constexpr int kPreRing = 4;                        // k-steps resident in LDS
 constexpr int kPreActB = kPreRows * 128;           // activation bytes of one k-step
-constexpr int kPreWB = kPreChunks * 2 * 512;       // packed values of one k-step
-constexpr int kPreMB = kPreChunks * 2 * 256;       // metadata of one k-step
-constexpr int kPreSB = kPreChunks * 128;           // scales of one k-step
+// Weight side of one k-step, per wave (two chunks): packed values of both k-blocks
+// (2 x 1 KiB), metadata (1 KiB), scales (256 B), contiguous so that one M0 value
+// serves the wave's four weight-side DMAs (instruction offsets 0/1024/2048/3072).
+constexpr int kPreWgtW = 3328;
+constexpr int kPreWgtB = 4 * kPreWgtW;              // weight side of one k-step
 constexpr int kPreActOff = 0;
-constexpr int kPreWOff = kPreActOff + kPreRing * kPreActB;
-constexpr int kPreMOff = kPreWOff + kPreRing * kPreWB;
-constexpr int kPreSOff = kPreMOff + kPreRing * kPreMB;
-constexpr int kPreLdsBytes = kPreSOff + kPreRing * kPreSB;
+constexpr int kPreWgtOff = kPreActOff + kPreRing * kPreActB;
+constexpr int kPreLdsBytes = kPreWgtOff + kPreRing * kPreWgtB;
+static_assert(kPreWgtW % 256 == 0, "wave blocks keep the bank pattern");
 
 // v_smfmac_f32_32x32x32_f16 with the accumulator in AGPRs; ABID selects the index
 // halfword.  Written as inline assembly because, for the intrinsic, the compiler
@@ -140,32 +141,45 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
     const int m = m0 + row < M ? m0 + row : M - 1;
     act_off[u] = ((uint32_t)m * (uint32_t)K + 8 * ls) * 2;
   }
-  // packed values of k-block kb: chunk cw + (lane >> 5), 16-byte piece lane & 31
-  const uint32_t wv_off = 512 * (uint32_t)(cw + (lane >> 5)) + 16 * (lane & 31);
+  // packed values of k-block kb: chunk cw + (lane >> 5); LDS slot s = lane & 31 holds
+  // the 16-byte piece 4 g8 + t (words (g8, t, 0..3)) with s = g8 + 8 (t >> 1) + 16 (t & 1),
+  // so that the two words a lane reads, (g8, 2h) and (g8, 2h + 1), lie 16 slots apart and
+  // the 32 lanes of each half-wave hit 32 distinct banks
+  const int wsl = lane & 31;
+  const uint32_t wv_off = 512 * (uint32_t)(cw + (lane >> 5)) + 16 * (4 * (wsl & 7) + 2 * ((wsl >> 3) & 1) + (wsl >> 4));
   const uint32_t wv_kb = 8 * (uint32_t)N;  // bytes per k-block row of values
   // metadata: k-block lane >> 5, chunk cw + ((lane >> 4) & 1), piece lane & 15
   const uint32_t mt_off = (lane >> 5) * 4 * (uint32_t)N + 256 * (uint32_t)(cw + ((lane >> 4) & 1)) + 16 * (lane & 15);
   // scales (4 bytes per lane): chunk cw + (lane >> 5), dword lane & 31
   const uint32_t sc_off = 128 * (uint32_t)(cw + (lane >> 5)) + 4 * (lane & 31);
 
-  const char* gA = reinterpret_cast<const char*>(a.A);
+  // Each DMA group shares one M0 value; the instruction offset 1024 u moves both the
+  // LDS and the global address, so the global bases are lowered by the group's largest
+  // offset and the per-lane offsets raised to match (none of them goes negative).
+  // Step offsets are 32-bit: the host keeps 2 M K + 4096 and K N / 4 below 2^32.
+  uint32_t act_v[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) act_v[u] = act_off[u] + 1024 * (3 - u);
+  const uint32_t wv1_v = wv_off + wv_kb - 1024;
+  const char* gA3 = reinterpret_cast<const char*>(a.A) - 3072;
   const char* gB = static_cast<const char*>(a.B);
-  const char* gM = static_cast<const char*>(a.meta);
-  const char* gS = reinterpret_cast<const char*>(a.s);
+  const char* gM2 = static_cast<const char*>(a.meta) - 2048;
+  const char* gS3 = reinterpret_cast<const char*>(a.s) - 3072;
+  const uint32_t strB = 16 * (uint32_t)N, strM = 8 * (uint32_t)N, strS = 2 * (uint32_t)N;
 
-  // DMA instruction i (0..NDMA-1) of local k-step s (clamped to the split's last) into
-  // ring slot q
-  auto dma = [&](int s, int q, int i) {
-    const int sc = ks0 + s < ks1 ? ks0 + s : ks1 - 1;
-    if (i < 4) {
-      dma16(lbase + kPreActOff + q * kPreActB + 1024 * (4 * w + i), act_off[i], gA + 128 * (size_t)sc);
-    } else if (i < 6) {
-      dma16(lbase + kPreWOff + q * kPreWB + 2048 * w + 1024 * (i - 4), wv_off + (i - 4) * wv_kb,
-                gB + 16 * (size_t)sc * N);
-    } else if (i == 6) {
-      dma16(lbase + kPreMOff + q * kPreMB + 1024 * w, mt_off, gM + 8 * (size_t)sc * N);
+  // DMA group g of local k-step s (clamped to the split's last) into ring slot q:
+  // g = 0 the step's activation rows of this wave (4 instructions), g = 1 its weight
+  // side (packed values of both k-blocks, metadata, and scales when grouped)
+  auto dma = [&](int s, int q, int g) {
+    const uint32_t sc = (uint32_t)(ks0 + s < ks1 ? ks0 + s : ks1 - 1);
+    if (g == 0) {
+      dma16x4(lbase + kPreActOff + q * kPreActB + 4096 * w, act_v, gA3 + 128 * sc);
     } else {
-      dma4(lbase + kPreSOff + q * kPreSB + 256 * w, sc_off, gS + 2 * (size_t)(sc >> 1) * N);
+      const uint32_t l = lbase + kPreWgtOff + q * kPreWgtB + kPreWgtW * w;
+      if constexpr (GROUPED)
+        dma_weights(l, wv_off, wv1_v, gB + sc * strB, mt_off, gM2 + sc * strM, sc_off, gS3 + (sc >> 1) * strS);
+      else
+        dma_weights_nos(l, wv_off, wv1_v, gB + sc * strB, mt_off, gM2 + sc * strM);
     }
   };
 
@@ -179,12 +193,13 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   for (int kb = 0; kb < 2; kb++)
 #pragma unroll
     for (int i = 0; i < 2; i++) b_off[kb][i] = kPreActOff + rho * 128 + 16 * ((4 * kb + 2 * h + i) ^ swz);
-  // packed words (kb, c, t = 2h) and (kb, c, 2h + 1) of column pair (8g8 + j, +4): + 16
-  const uint32_t w_rd = kPreWOff + 2048 * w + 4 * (16 * g8 + 8 * h + j);
+  // packed words (kb, c, t = 2h) and (kb, c, 2h + 1) of column pair (8g8 + j, +4): slots
+  // g8 + 8h and g8 + 8h + 16 (+ 256 bytes)
+  const uint32_t w_rd = kPreWgtOff + kPreWgtW * w + 16 * (g8 + 8 * h) + 4 * j;
   // metadata unit of the column pair
-  const uint32_t m_rd = kPreMOff + 1024 * w + 8 * (16 * (j >> 1) + 2 * g8 + (j & 1));
+  const uint32_t m_rd = kPreWgtOff + kPreWgtW * w + 2048 + 8 * (16 * (j >> 1) + 2 * g8 + (j & 1));
   // scales of columns 8g8 + j (+4): slots 8g8 + 2j, + 1
-  const uint32_t s_rd = kPreSOff + 256 * w + 16 * g8 + 4 * j;
+  const uint32_t s_rd = kPreWgtOff + kPreWgtW * w + 3072 + 16 * g8 + 4 * j;
   // index halfwords of both halves: [d0.b(h), d1.b(h), d0.b(2+h), d1.b(2+h)]
   const uint32_t isel = h ? 0x07030501u : 0x06020400u;
 
@@ -215,20 +230,22 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   };
 
   // raw operands of the next k-step's dequantization, combo k = (kb, c) = (k >> 1, k & 1)
-  uint32_t rw[4][2];  // packed words t = 2h, 2h + 1
-  u32x2 rm[4];        // metadata unit
-  uint32_t rs[2];     // scales of columns (8g8 + j, + 4), per chunk
-  auto read_raw = [&](int q, int k) {
+  // raw operands by k-step parity: those of step s+1 are dequantized during step s,
+  // and read during step s-1 (a wave reads only the weight side it loaded itself)
+  uint32_t rw[2][4][2];  // packed words t = 2h, 2h + 1
+  u32x2 rm[2][4];        // metadata unit
+  uint32_t rs[2][2];     // scales of columns (8g8 + j, + 4), per chunk
+  auto read_raw = [&](int q, int k, int par) {
     const int kb = k >> 1, c = k & 1;
-    const uint8_t* pw = lds + w_rd + q * kPreWB + 1024 * kb + 512 * c;
-    rw[k][0] = *reinterpret_cast<const uint32_t*>(pw);
-    rw[k][1] = *reinterpret_cast<const uint32_t*>(pw + 16);
-    rm[k] = *reinterpret_cast<const u32x2*>(lds + m_rd + q * kPreMB + 512 * kb + 256 * c);
+    const uint8_t* pw = lds + w_rd + q * kPreWgtB + 1024 * kb + 512 * c;
+    rw[par][k][0] = *reinterpret_cast<const uint32_t*>(pw);
+    rw[par][k][1] = *reinterpret_cast<const uint32_t*>(pw + 256);
+    rm[par][k] = *reinterpret_cast<const u32x2*>(lds + m_rd + q * kPreWgtB + 512 * kb + 256 * c);
   };
-  auto read_scales = [&](int q) {
+  auto read_scales = [&](int q, int par) {
     if constexpr (GROUPED) {
 #pragma unroll
-      for (int c = 0; c < 2; c++) rs[c] = *reinterpret_cast<const uint32_t*>(lds + s_rd + q * kPreSB + 128 * c);
+      for (int c = 0; c < 2; c++) rs[par][c] = *reinterpret_cast<const uint32_t*>(lds + s_rd + q * kPreWgtB + 128 * c);
     }
   };
 
@@ -242,8 +259,8 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
     const half2_t k1032 = {(_Float16)1032.f, (_Float16)1032.f};
     const half2_t k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
     const half2_t km72 = {(_Float16)-72.f, (_Float16)-72.f};
-    const uint32_t w0 = rw[k][0], w1 = rw[k][1];
-    const half2_t scv = __builtin_bit_cast(half2_t, rs[c]);
+    const uint32_t w0 = rw[par][k][0], w1 = rw[par][k][1];
+    const half2_t scv = __builtin_bit_cast(half2_t, rs[par][c]);
     auto scl = [&](int hf, int i) {
       if constexpr (GROUPED) {
         const _Float16 sv = hf ? scv.y : scv.x;
@@ -290,7 +307,7 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
       default:
         scl(1, 2);
         scl(1, 3);
-        ix[par][kb][c] = __builtin_amdgcn_perm(rm[k].y, rm[k].x, isel);
+        ix[par][kb][c] = __builtin_amdgcn_perm(rm[par][k].y, rm[par][k].x, isel);
 #pragma unroll
         for (int hf = 0; hf < 2; hf++)
           av[par][kb][2 * c + hf] = (half8_t){dp[hf][0].x, dp[hf][0].y, dp[hf][1].x, dp[hf][1].y,
@@ -302,11 +319,11 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   // ---- k-step s in ring slot Q = s & 3 (slot Q+1: step s+1, slot Q+3: step s+3):
   //   barrier: this wave's DMAs of step s+1 have landed, every wave has finished step
   //   s-1 (its reads of slot Q+3);
-  //   32 regions r = (kb, rg, c, hf), each one MFMA plus a share of: the DMAs of step
-  //   s+3 (r < NDMA); at hf = c = 0 the read of B fragment f+2 (f = 4kb + rg; from
-  //   step s+1 past 7); at r < 4 the raw words and metadata of step s+1, combo r, and
-  //   at r = 4 its scales; at r >= 4 slice (r-4) % 7 of dequantizing combo (r-4) / 7
-  //   of step s+1.
+  //   32 regions r = (kb, rg, c, hf), each one MFMA plus a share of: DMA group r >> 1
+  //   of step s+3 (r = 1, 3); at hf = c = 0 the read of B fragment f+2 (f = 4kb + rg; from
+  //   step s+1 past 7); at 16 <= r < 20 the raw words and metadata of step s+2, combo
+  //   r-16 (after waiting for this wave's DMAs of step s+2), and at r = 20 its scales;
+  //   at r >= 4 slice (r-4) % 7 of dequantizing combo (r-4) / 7 of step s+1.
   // Steps past the last are skipped (uniform); the DMAs are clamped, so the vmcnt of
   // every barrier counts exactly the DMAs of one step. ----
   auto step = [&](int s, auto qc) {
@@ -319,9 +336,10 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
       else pre_smfmac<0>(acc[rg][af], av[P][kb][af], bv[f & 3], ix[P][kb][c]);
       __builtin_amdgcn_sched_barrier(0);  // the region's work follows its MFMA
       if (af == 0) bv[(f + 2) & 3] = read_b(f + 2 < 8 ? Q : QN, (f + 2) & 7);
-      if (r < NDMA) dma(s + 3, QD, r);
-      if (r < 4) read_raw(QN, r);
-      if (r == 4) read_scales(QN);
+      if (r == 1 || r == 3) dma(s + 3, QD, r >> 1);
+      if (r == 16) wait_vm<NDMA>();  // this wave's DMAs of step s+2 have landed
+      if (r >= 16 && r < 20) read_raw((Q + 2) & 3, r - 16, P);
+      if (r == 20) read_scales((Q + 2) & 3, P);
       if (r >= 4) dq_slice((r - 4) / 7, (r - 4) % 7, P ^ 1);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -332,15 +350,18 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
 #pragma unroll
   for (int s = 0; s < 3; s++)
 #pragma unroll
-    for (int i = 0; i < NDMA; i++) dma(s, s, i);
+    for (int g = 0; g < 2; g++) dma(s, s, g);
   pre_step_barrier<NDMA>();
 #pragma unroll
-  for (int k = 0; k < 4; k++) read_raw(0, k);
-  read_scales(0);
+  for (int k = 0; k < 4; k++) read_raw(0, k, 0);
+  read_scales(0, 0);
 #pragma unroll
   for (int k = 0; k < 4; k++)
 #pragma unroll
     for (int sl = 0; sl < 7; sl++) dq_slice(k, sl, 0);
+#pragma unroll
+  for (int k = 0; k < 4; k++) read_raw(1, k, 1);
+  read_scales(1, 1);
   bv[0] = read_b(0, 0);
   bv[1] = read_b(0, 1);
   __builtin_amdgcn_sched_barrier(0);
