@@ -129,54 +129,45 @@ __device__ __forceinline__ float4_t smfmac64(half8_t a, half16_t b, float4_t c, 
   return __builtin_amdgcn_smfmac_f32_16x16x64_f16(a, b, c, (int)idx, 0, ABID);
 }
 
-// LDS-DMA: every lane copies 16 (4) bytes from base + voff to LDS byte address
-// lds + 16 (4) * lane.  Tracked by vmcnt, like any global load; `lds` must be
-// wave-uniform.  M0 is set here (one wait state before the DMA reads it).
-__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, const void* base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
-}
+// LDS-DMA (global_load_lds_*): every lane copies 16 (or 4) bytes from a global
+// address to LDS byte address M0 + instruction offset + 16 (or 4) * lane; the
+// instruction offset applies to both addresses.  Tracked by vmcnt, like any global
+// load; the LDS address must be wave-uniform.  M0 is set in the same statement (one
+// wait state before the first DMA reads it).
 
-// Four LDS-DMAs of 16 bytes per lane into lds + 1024 u + 16 lane (u = 0..3) from
-// base + v[u] + 1024 u: one M0 value, instruction offsets 0/1024/2048/3072 (applied to
-// both addresses).
-__device__ __forceinline__ void dma16x4(uint32_t lds, const uint32_t (&v)[4], const void* base) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %5\n\t"
-      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
-      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
-      "global_load_lds_dwordx4 %4, %5 offset:3072" ::"s"(lds),
-      "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "s"(base)
-      : "memory", "m0");
-}
-// The weight side of a k-step for one wave, into lds + [0, 3328): 16 bytes per lane
-// from bw + v0 (-> lds), bw + v1 + 1024 (-> + 1024) and bm + vm + 2048 (-> + 2048),
-// then 4 bytes per lane from bs + vs + 3072 (-> + 3072).
-__device__ __forceinline__ void dma_weights(uint32_t lds, uint32_t v0, uint32_t v1, const void* bw, uint32_t vm,
-                                            const void* bm, uint32_t vs, const void* bs) {
+// Two DMAs of 16 bytes per lane into lds + 1024 u + 16 lane (u = 0, 1) from
+// base + v[u] + 1024 u.
+__device__ __forceinline__ void dma16x2(uint32_t lds, const uint32_t (&v)[2], const void* base) {
   asm volatile(
       "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
       "global_load_lds_dwordx4 %1, %3\n\t"
-      "global_load_lds_dwordx4 %2, %3 offset:1024\n\t"
-      "global_load_lds_dwordx4 %4, %5 offset:2048\n\t"
-      "global_load_lds_dword %6, %7 offset:3072" ::"s"(lds),
-      "v"(v0), "v"(v1), "s"(bw), "v"(vm), "s"(bm), "v"(vs), "s"(bs)
+      "global_load_lds_dwordx4 %2, %3 offset:1024" ::"s"(lds),
+      "v"(v[0]), "v"(v[1]), "s"(base)
       : "memory", "m0");
 }
-// As dma_weights without the scales.
-__device__ __forceinline__ void dma_weights_nos(uint32_t lds, uint32_t v0, uint32_t v1, const void* bw, uint32_t vm,
-                                                const void* bm) {
+// One wave's weight side of a k-step, into lds + [0, 1792): 16 bytes per lane from
+// bw + vw (-> lds + 16 lane), 4 bytes per lane from bm + vm0 + 1024 (-> + 1024) and
+// bm + vm1 + 1280 (-> + 1280), then 4 bytes per lane from bs + vs + 1536 (-> + 1536).
+__device__ __forceinline__ void dma_chunk(uint32_t lds, uint32_t vw, const void* bw, uint32_t vm0, uint32_t vm1,
+                                          const void* bm, uint32_t vs, const void* bs) {
   asm volatile(
       "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %3\n\t"
-      "global_load_lds_dwordx4 %2, %3 offset:1024\n\t"
-      "global_load_lds_dwordx4 %4, %5 offset:2048" ::"s"(lds),
-      "v"(v0), "v"(v1), "s"(bw), "v"(vm), "s"(bm)
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "global_load_lds_dword %3, %5 offset:1024\n\t"
+      "global_load_lds_dword %4, %5 offset:1280\n\t"
+      "global_load_lds_dword %6, %7 offset:1536" ::"s"(lds),
+      "v"(vw), "s"(bw), "v"(vm0), "v"(vm1), "s"(bm), "v"(vs), "s"(bs)
+      : "memory", "m0");
+}
+// As dma_chunk without the scales.
+__device__ __forceinline__ void dma_chunk_nos(uint32_t lds, uint32_t vw, const void* bw, uint32_t vm0, uint32_t vm1,
+                                              const void* bm) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "global_load_lds_dword %3, %5 offset:1024\n\t"
+      "global_load_lds_dword %4, %5 offset:1280" ::"s"(lds),
+      "v"(vw), "s"(bw), "v"(vm0), "v"(vm1), "s"(bm)
       : "memory", "m0");
 }
 

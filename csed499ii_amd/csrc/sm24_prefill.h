@@ -1,24 +1,26 @@
 // Prefill-sized (large M) 2:4 INT4 x FP16 GEMM for gfx950, MFMA-bound.
 //
-// Workgroup tile: 512 output columns (8 chunks of 64) x 128 batch rows, 4 waves, one
-// per SIMD; wave w owns chunks 2w, 2w+1 (128 columns) for all 128 rows as 4 x 4
-// v_smfmac_f32_32x32x32_f16 accumulators (256 AGPRs).  K advances in steps of 64 (two
-// 32-deep k-blocks); one k-step is 32 MFMAs per wave.
+// Workgroup tile: 512 output columns (8 chunks of 64) x 128 batch rows, 8 waves, two
+// per SIMD; wave w owns chunk w (64 columns) for all 128 rows as 4 x 2
+// v_smfmac_f32_32x32x32_f16 accumulators (128 AGPRs).  K advances in steps of 64 (two
+// 32-deep k-blocks); one k-step is 16 MFMAs per wave.
 //
-// Why 32x32x32.  Measured on MI355X with one wave per SIMD: an smfmac keeps the
-// SIMD's VALU issue busy for most of its own duration (13 of ~17 cycles for
-// 16x16x64), so VALU work overlaps an MFMA only up to ~1 instruction per 16x16x64
-// but ~5 per 32x32x32, which reads the same operand registers for twice the flops.
-// Dequantization costs 13 VALU instructions per 8-value weight fragment; with
-// 32x32x32 the k-step needs ~3.6 VALU instructions per MFMA, inside that budget.
+// Why two waves per SIMD.  Measured on MI355X (random operands): a 32x32x32 smfmac
+// takes ~35 cycles, and the VALU can issue ~4 instructions of 4 cycles beside it.
+// With one wave per SIMD every other instruction (LDS read, LDS-DMA, SALU, wait) is
+// issued in order by the same wave and adds ~3-10 cycles to its MFMA; with two waves
+// the other wave's MFMA hides them, and a mix of 4 VALU + 1 ds_read_b128 + DMA per
+// MFMA runs at ~37 cycles per MFMA instead of ~54.  Dequantization stays at ~3.4 VALU
+// instructions per MFMA because each wave still covers all 128 rows of its columns
+// (13 VALU per 8-value weight fragment, reused by 4 B fragments).
 //
 // Operand routes (all global reads are LDS-DMA: no staging registers, no staging
 // VALU; a ring of 4 k-steps, filled 3 steps ahead, one barrier per k-step):
 //  * activations: 128 rows x 128 bytes per k-step; 16-byte pieces stored with the
 //    logical slot XOR ((row >> 1) & 7) so that the B-fragment reads are free of bank
 //    conflicts; a B lane (row, h) reads the 32 contiguous bytes of k 16h..16h+15;
-//  * packed values, metadata, scales: the raw global layout of each wave's own 2
-//    chunks (512 + 256 + 128 bytes per chunk and k-step), read per lane as needed.
+//  * packed values, metadata, scales: the raw global layout of each wave's own chunk
+//    (512 + 256 bytes per k-block, 128 bytes of scales per group), read per lane.
 //
 // MFMA k order.  For a 32-deep k-block, A lane group h (lanes 32h..32h+31) holds MFMA
 // groups 4h..4h+3 = real groups 2h, 2h+1, 2h+4, 2h+5, which makes:
@@ -43,23 +45,26 @@ struct IntC {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPreRows = 128;  // batch rows per tile
-constexpr int kPreChunks = 8;  // 64-column chunks per tile
+constexpr int kPreChunks = 8;  // 64-column chunks per tile = waves per workgroup
 static_assert(64 * kPreChunks == kPreTileCols, "tile width");
+constexpr int kPreThreads = 64 * kPreChunks;
 constexpr int kPreRing = 4;                        // k-steps resident in LDS
 constexpr int kPreActB = kPreRows * 128;           // activation bytes of one k-step
-// Weight side of one k-step, per wave (two chunks): packed values of both k-blocks
-// (2 x 1 KiB), metadata (1 KiB), scales (256 B), contiguous so that one M0 value
-// serves the wave's four weight-side DMAs (instruction offsets 0/1024/2048/3072).
-constexpr int kPreWgtW = 3328;
-constexpr int kPreWgtB = 4 * kPreWgtW;              // weight side of one k-step
+// Weight side of one k-step, per wave (one chunk): packed values of both k-blocks
+// (1 KiB), metadata of both k-blocks (2 x 256 B), scales of the chunk pair (256 B),
+// contiguous so that one M0 value serves the wave's weight-side DMAs (instruction
+// offsets 0/1024/1280/1536).
+constexpr int kPreWgtW = 1792;
+constexpr int kPreWgtB = kPreChunks * kPreWgtW;    // weight side of one k-step
 constexpr int kPreActOff = 0;
 constexpr int kPreWgtOff = kPreActOff + kPreRing * kPreActB;
 constexpr int kPreLdsBytes = kPreWgtOff + kPreRing * kPreWgtB;
 static_assert(kPreWgtW % 256 == 0, "wave blocks keep the bank pattern");
+static_assert(kPreLdsBytes <= 160 * 1024, "LDS");
 
 // v_smfmac_f32_32x32x32_f16 with the accumulator in AGPRs; ABID selects the index
 // halfword.  Written as inline assembly because, for the intrinsic, the compiler
-// splits 256 accumulator registers between VGPRs and AGPRs and copies them around
+// splits the accumulator registers between VGPRs and AGPRs and copies them around
 // the MFMAs.  Assembly takes the MFMA out of the compiler's hazard tracking, so the
 // kernel keeps the gfx950 rules by construction: an operand VGPR written by a VALU
 // instruction is read at least two instructions later (operands come from LDS
@@ -84,16 +89,16 @@ __device__ __forceinline__ void pre_step_barrier() {
 }
 
 template <bool GROUPED>
-__global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a) {
   constexpr int MT = kPreRows, CT = kPreChunks;
-  constexpr int NDMA = GROUPED ? 8 : 7;  // DMA instructions per wave and k-step
+  constexpr int NDMA = GROUPED ? 6 : 5;  // DMA instructions per wave and k-step
   __shared__ __attribute__((aligned(16))) uint8_t lds[kPreLdsBytes];
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const uint32_t lbase = (uint32_t)(size_t)(lds_u8*)lds;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // chunk pair of this wave
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // chunk of this wave
   const int M = a.M, N = a.N, K = a.K;
   const int nks = K >> 6;  // even: the host requires K % 128 == 0
 
@@ -126,60 +131,57 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   }
   const int c0 = tn * CT;         // first chunk of the tile
   const int m0 = tm * MT;         // first batch row
-  const int cw = c0 + 2 * w;      // first chunk of this wave
+  const int cw = c0 + w;          // chunk of this wave
 
   // ---- DMA sources: per-lane byte offsets from per-k-step bases ----
-  // activations: instruction u of wave w fills pieces 64(4w+u) + lane of the step's
+  // activations: instruction u of wave w fills pieces 64(2w + u) + lane of the step's
   // 1024 16-byte pieces; piece P = row P >> 3, physical slot P & 7, which holds the
   // logical slot (P & 7) ^ ((row >> 1) & 7).  Rows past M repeat row M-1 (never
-  // stored); M*K < 2^31 is checked by the host.
-  uint32_t act_off[4];
+  // stored); the host keeps 2 M K + 4096 below 2^32.
+  uint32_t act_v[2];
 #pragma unroll
-  for (int u = 0; u < 4; u++) {
-    const int p = 64 * (4 * w + u) + lane, row = p >> 3;
+  for (int u = 0; u < 2; u++) {
+    const int p = 64 * (2 * w + u) + lane, row = p >> 3;
     const int ls = (p & 7) ^ ((row >> 1) & 7);
     const int m = m0 + row < M ? m0 + row : M - 1;
-    act_off[u] = ((uint32_t)m * (uint32_t)K + 8 * ls) * 2;
+    // + 1024 (1 - u): instruction u carries offset 1024 u, the base is lowered by 1024
+    act_v[u] = ((uint32_t)m * (uint32_t)K + 8 * ls) * 2 + 1024 * (1 - u);
   }
-  // packed values of k-block kb: chunk cw + (lane >> 5); LDS slot s = lane & 31 holds
-  // the 16-byte piece 4 g8 + t (words (g8, t, 0..3)) with s = g8 + 8 (t >> 1) + 16 (t & 1),
-  // so that the two words a lane reads, (g8, 2h) and (g8, 2h + 1), lie 16 slots apart and
-  // the 32 lanes of each half-wave hit 32 distinct banks
+  // packed values: k-block lane >> 5 of chunk cw; LDS slot s = lane & 31 holds the
+  // 16-byte piece 4 g8 + t (words (g8, t, 0..3)) with s = g8 + 8 (t >> 1) + 16 (t & 1),
+  // so that the two words a lane reads, (g8, 2h) and (g8, 2h + 1), lie 16 slots apart
+  // and the 32 lanes of each half-wave hit 32 distinct banks
   const int wsl = lane & 31;
-  const uint32_t wv_off = 512 * (uint32_t)(cw + (lane >> 5)) + 16 * (4 * (wsl & 7) + 2 * ((wsl >> 3) & 1) + (wsl >> 4));
-  const uint32_t wv_kb = 8 * (uint32_t)N;  // bytes per k-block row of values
-  // metadata: k-block lane >> 5, chunk cw + ((lane >> 4) & 1), piece lane & 15
-  const uint32_t mt_off = (lane >> 5) * 4 * (uint32_t)N + 256 * (uint32_t)(cw + ((lane >> 4) & 1)) + 16 * (lane & 15);
-  // scales (4 bytes per lane): chunk cw + (lane >> 5), dword lane & 31
-  const uint32_t sc_off = 128 * (uint32_t)(cw + (lane >> 5)) + 4 * (lane & 31);
+  const uint32_t wv_v = (lane >> 5) * 8 * (uint32_t)N + 512 * (uint32_t)cw +
+                        16 * (4 * (wsl & 7) + 2 * ((wsl >> 3) & 1) + (wsl >> 4));
+  // metadata (4 bytes per lane) of k-block 0 of chunk cw (base lowered by 1024), and
+  // of k-block 1 (4N bytes on; instruction offset 1280)
+  const uint32_t mt_v0 = 256 * (uint32_t)cw + 4 * lane;
+  const uint32_t mt_v1 = mt_v0 + 4 * (uint32_t)N - 256;
+  // scales (4 bytes per lane) of the chunk pair (cw & ~1, cw | 1) (base lowered by 1536)
+  const uint32_t sc_v = 128 * (uint32_t)(cw & ~1) + 4 * lane;
 
-  // Each DMA group shares one M0 value; the instruction offset 1024 u moves both the
-  // LDS and the global address, so the global bases are lowered by the group's largest
-  // offset and the per-lane offsets raised to match (none of them goes negative).
-  // Step offsets are 32-bit: the host keeps 2 M K + 4096 and K N / 4 below 2^32.
-  uint32_t act_v[4];
-#pragma unroll
-  for (int u = 0; u < 4; u++) act_v[u] = act_off[u] + 1024 * (3 - u);
-  const uint32_t wv1_v = wv_off + wv_kb - 1024;
-  const char* gA3 = reinterpret_cast<const char*>(a.A) - 3072;
+  const char* gA1 = reinterpret_cast<const char*>(a.A) - 1024;
   const char* gB = static_cast<const char*>(a.B);
-  const char* gM2 = static_cast<const char*>(a.meta) - 2048;
-  const char* gS3 = reinterpret_cast<const char*>(a.s) - 3072;
+  const char* gM1 = static_cast<const char*>(a.meta) - 1024;
+  const char* gS1 = reinterpret_cast<const char*>(a.s) - 1536;
   const uint32_t strB = 16 * (uint32_t)N, strM = 8 * (uint32_t)N, strS = 2 * (uint32_t)N;
 
   // DMA group g of local k-step s (clamped to the split's last) into ring slot q:
-  // g = 0 the step's activation rows of this wave (4 instructions), g = 1 its weight
-  // side (packed values of both k-blocks, metadata, and scales when grouped)
+  // g = 0 this wave's share of the step's activation rows (2 instructions), g = 1 the
+  // weight side of its chunk (packed values, metadata of both k-blocks, and the
+  // scales of its chunk pair when grouped).  Step offsets are 32-bit: the host keeps
+  // K N / 4 below 2^32.
   auto dma = [&](int s, int q, int g) {
     const uint32_t sc = (uint32_t)(ks0 + s < ks1 ? ks0 + s : ks1 - 1);
     if (g == 0) {
-      dma16x4(lbase + kPreActOff + q * kPreActB + 4096 * w, act_v, gA3 + 128 * sc);
+      dma16x2(lbase + kPreActOff + q * kPreActB + 2048 * w, act_v, gA1 + 128 * sc);
     } else {
       const uint32_t l = lbase + kPreWgtOff + q * kPreWgtB + kPreWgtW * w;
       if constexpr (GROUPED)
-        dma_weights(l, wv_off, wv1_v, gB + sc * strB, mt_off, gM2 + sc * strM, sc_off, gS3 + (sc >> 1) * strS);
+        dma_chunk(l, wv_v, gB + sc * strB, mt_v0, mt_v1, gM1 + sc * strM, sc_v, gS1 + (sc >> 1) * strS);
       else
-        dma_weights_nos(l, wv_off, wv1_v, gB + sc * strB, mt_off, gM2 + sc * strM);
+        dma_chunk_nos(l, wv_v, gB + sc * strB, mt_v0, mt_v1, gM1 + sc * strM);
     }
   };
 
@@ -193,13 +195,14 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   for (int kb = 0; kb < 2; kb++)
 #pragma unroll
     for (int i = 0; i < 2; i++) b_off[kb][i] = kPreActOff + rho * 128 + 16 * ((4 * kb + 2 * h + i) ^ swz);
-  // packed words (kb, c, t = 2h) and (kb, c, 2h + 1) of column pair (8g8 + j, +4): slots
-  // g8 + 8h and g8 + 8h + 16 (+ 256 bytes)
-  const uint32_t w_rd = kPreWgtOff + kPreWgtW * w + 16 * (g8 + 8 * h) + 4 * j;
-  // metadata unit of the column pair
-  const uint32_t m_rd = kPreWgtOff + kPreWgtW * w + 2048 + 8 * (16 * (j >> 1) + 2 * g8 + (j & 1));
-  // scales of columns 8g8 + j (+4): slots 8g8 + 2j, + 1
-  const uint32_t s_rd = kPreWgtOff + kPreWgtW * w + 3072 + 16 * g8 + 4 * j;
+  const uint32_t wblk = kPreWgtOff + kPreWgtW * w;
+  // packed words (kb, t = 2h) and (kb, 2h + 1) of column pair (8g8 + j, +4): slots
+  // g8 + 8h and g8 + 8h + 16 (+ 256 bytes) of k-block kb's 512 bytes
+  const uint32_t w_rd = wblk + 16 * (g8 + 8 * h) + 4 * j;
+  // metadata unit of the column pair in k-block kb's 256 bytes
+  const uint32_t m_rd = wblk + 1024 + 8 * (16 * (j >> 1) + 2 * g8 + (j & 1));
+  // scales of columns 8g8 + j (+4): slots 8g8 + 2j, + 1 of this chunk's 128 bytes
+  const uint32_t s_rd = wblk + 1536 + 128 * (cw & 1) + 16 * g8 + 4 * j;
   // index halfwords of both halves: [d0.b(h), d1.b(h), d0.b(2+h), d1.b(2+h)]
   const uint32_t isel = h ? 0x07030501u : 0x06020400u;
 
@@ -208,16 +211,16 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
   asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
 
-  half8_t av[2][2][4];   // [parity][kb][2c + hf] dequantized weight fragments
-  uint32_t ix[2][2][2];  // [parity][kb][c] index halfwords (hf = abid)
-  half16_t bv[4];        // B fragments, ring by fragment number kb*4 + rg
-  f32x16 acc[4][4];      // [rg][2c + hf]
+  half8_t av[2][2][2];  // [parity][kb][hf] dequantized weight fragments
+  uint32_t ix[2][2];    // [parity][kb] index halfwords (hf = abid)
+  half16_t bv[4];       // B fragments, ring by fragment number kb*4 + rg
+  f32x16 acc[4][2];     // [rg][hf]
 #pragma unroll
   for (int rg = 0; rg < 4; rg++)
 #pragma unroll
-    for (int af = 0; af < 4; af++) {
-      acc[rg][af] = (f32x16){};
-      asm volatile("" : "+a"(acc[rg][af]));
+    for (int hf = 0; hf < 2; hf++) {
+      acc[rg][hf] = (f32x16){};
+      asm volatile("" : "+a"(acc[rg][hf]));
     }
 
   auto read_b = [&](int q, int f) -> half16_t {
@@ -229,38 +232,31 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
   };
 
-  // raw operands of the next k-step's dequantization, combo k = (kb, c) = (k >> 1, k & 1)
-  // raw operands by k-step parity: those of step s+1 are dequantized during step s,
-  // and read during step s-1 (a wave reads only the weight side it loaded itself)
-  uint32_t rw[2][4][2];  // packed words t = 2h, 2h + 1
-  u32x2 rm[2][4];        // metadata unit
-  uint32_t rs[2][2];     // scales of columns (8g8 + j, + 4), per chunk
-  auto read_raw = [&](int q, int k, int par) {
-    const int kb = k >> 1, c = k & 1;
-    const uint8_t* pw = lds + w_rd + q * kPreWgtB + 1024 * kb + 512 * c;
-    rw[par][k][0] = *reinterpret_cast<const uint32_t*>(pw);
-    rw[par][k][1] = *reinterpret_cast<const uint32_t*>(pw + 256);
-    rm[par][k] = *reinterpret_cast<const u32x2*>(lds + m_rd + q * kPreWgtB + 512 * kb + 256 * c);
+  // raw operands of the next k-step's dequantization, per k-block
+  uint32_t rw[2][2];  // packed words t = 2h, 2h + 1
+  u32x2 rm[2];        // metadata unit
+  uint32_t rs = 0;    // scales of columns (8g8 + j, + 4)
+  auto read_raw = [&](int q, int kb) {
+    const uint8_t* pw = lds + w_rd + q * kPreWgtB + 512 * kb;
+    rw[kb][0] = *reinterpret_cast<const uint32_t*>(pw);
+    rw[kb][1] = *reinterpret_cast<const uint32_t*>(pw + 256);
+    rm[kb] = *reinterpret_cast<const u32x2*>(lds + m_rd + q * kPreWgtB + 256 * kb);
   };
-  auto read_scales = [&](int q, int par) {
-    if constexpr (GROUPED) {
-#pragma unroll
-      for (int c = 0; c < 2; c++) rs[par][c] = *reinterpret_cast<const uint32_t*>(lds + s_rd + q * kPreWgtB + 128 * c);
-    }
+  auto read_scales = [&](int q) {
+    if constexpr (GROUPED) rs = *reinterpret_cast<const uint32_t*>(lds + s_rd + q * kPreWgtB);
   };
 
-  // ---- dequantization of combo k into av[par][kb][2c + hf], ix[par][kb][c], in seven
+  // ---- dequantization of k-block kb into av[par][kb][hf], ix[par][kb], in seven
   // slices of at most four VALU instructions: word halves -> magic-number halves
   // 1024 + q (low nibbles) or 1024 + 16q (high nibbles) -> q - 8 -> times scale ----
   uint32_t dx[2][4];
   half2_t dp[2][4];
-  auto dq_slice = [&](int k, int sl, int par) {
-    const int kb = k >> 1, c = k & 1;
+  auto dq_slice = [&](int kb, int sl, int par) {
     const half2_t k1032 = {(_Float16)1032.f, (_Float16)1032.f};
     const half2_t k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
     const half2_t km72 = {(_Float16)-72.f, (_Float16)-72.f};
-    const uint32_t w0 = rw[par][k][0], w1 = rw[par][k][1];
-    const half2_t scv = __builtin_bit_cast(half2_t, rs[par][c]);
+    const uint32_t w0 = rw[kb][0], w1 = rw[kb][1];
+    const half2_t scv = __builtin_bit_cast(half2_t, rs);
     auto scl = [&](int hf, int i) {
       if constexpr (GROUPED) {
         const _Float16 sv = hf ? scv.y : scv.x;
@@ -307,11 +303,11 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
       default:
         scl(1, 2);
         scl(1, 3);
-        ix[par][kb][c] = __builtin_amdgcn_perm(rm[par][k].y, rm[par][k].x, isel);
+        ix[par][kb] = __builtin_amdgcn_perm(rm[kb].y, rm[kb].x, isel);
 #pragma unroll
         for (int hf = 0; hf < 2; hf++)
-          av[par][kb][2 * c + hf] = (half8_t){dp[hf][0].x, dp[hf][0].y, dp[hf][1].x, dp[hf][1].y,
-                                              dp[hf][2].x, dp[hf][2].y, dp[hf][3].x, dp[hf][3].y};
+          av[par][kb][hf] = (half8_t){dp[hf][0].x, dp[hf][0].y, dp[hf][1].x, dp[hf][1].y,
+                                      dp[hf][2].x, dp[hf][2].y, dp[hf][3].x, dp[hf][3].y};
         break;
     }
   };
@@ -319,28 +315,27 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
   // ---- k-step s in ring slot Q = s & 3 (slot Q+1: step s+1, slot Q+3: step s+3):
   //   barrier: this wave's DMAs of step s+1 have landed, every wave has finished step
   //   s-1 (its reads of slot Q+3);
-  //   32 regions r = (kb, rg, c, hf), each one MFMA plus a share of: DMA group r >> 1
-  //   of step s+3 (r = 1, 3); at hf = c = 0 the read of B fragment f+2 (f = 4kb + rg; from
-  //   step s+1 past 7); at 16 <= r < 20 the raw words and metadata of step s+2, combo
-  //   r-16 (after waiting for this wave's DMAs of step s+2), and at r = 20 its scales;
-  //   at r >= 4 slice (r-4) % 7 of dequantizing combo (r-4) / 7 of step s+1.
+  //   16 regions r = (kb, rg, hf), each one MFMA plus a share of: DMA group r >> 1 of
+  //   step s+3 (r = 1, 3); at hf = 0 the read of B fragment f+2 (f = 4kb + rg; from
+  //   step s+1 past 7); at r < 2 the raw words and metadata of step s+1, k-block r,
+  //   and at r = 2 its scales; at r >= 2 slice (r-2) % 7 of dequantizing k-block
+  //   (r-2) / 7 of step s+1.
   // Steps past the last are skipped (uniform); the DMAs are clamped, so the vmcnt of
   // every barrier counts exactly the DMAs of one step. ----
   auto step = [&](int s, auto qc) {
     constexpr int Q = decltype(qc)::value, P = Q & 1, QN = (Q + 1) & 3, QD = (Q + 3) & 3;
     pre_step_barrier<NDMA>();
 #pragma unroll
-    for (int r = 0; r < 32; r++) {
-      const int kb = r >> 4, rg = (r >> 2) & 3, af = r & 3, c = af >> 1, hf = af & 1, f = r >> 2;
-      if (hf) pre_smfmac<1>(acc[rg][af], av[P][kb][af], bv[f & 3], ix[P][kb][c]);
-      else pre_smfmac<0>(acc[rg][af], av[P][kb][af], bv[f & 3], ix[P][kb][c]);
+    for (int r = 0; r < 16; r++) {
+      const int kb = r >> 3, rg = (r >> 1) & 3, hf = r & 1, f = r >> 1;
+      if (hf) pre_smfmac<1>(acc[rg][hf], av[P][kb][hf], bv[f & 3], ix[P][kb]);
+      else pre_smfmac<0>(acc[rg][hf], av[P][kb][hf], bv[f & 3], ix[P][kb]);
       __builtin_amdgcn_sched_barrier(0);  // the region's work follows its MFMA
-      if (af == 0) bv[(f + 2) & 3] = read_b(f + 2 < 8 ? Q : QN, (f + 2) & 7);
+      if (hf == 0) bv[(f + 2) & 3] = read_b(f + 2 < 8 ? Q : QN, (f + 2) & 7);
       if (r == 1 || r == 3) dma(s + 3, QD, r >> 1);
-      if (r == 16) wait_vm<NDMA>();  // this wave's DMAs of step s+2 have landed
-      if (r >= 16 && r < 20) read_raw((Q + 2) & 3, r - 16, P);
-      if (r == 20) read_scales((Q + 2) & 3, P);
-      if (r >= 4) dq_slice((r - 4) / 7, (r - 4) % 7, P ^ 1);
+      if (r < 2) read_raw(QN, r);
+      if (r == 2) read_scales(QN);
+      if (r >= 2) dq_slice((r - 2) / 7, (r - 2) % 7, P ^ 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -353,15 +348,12 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
     for (int g = 0; g < 2; g++) dma(s, s, g);
   pre_step_barrier<NDMA>();
 #pragma unroll
-  for (int k = 0; k < 4; k++) read_raw(0, k, 0);
-  read_scales(0, 0);
+  for (int kb = 0; kb < 2; kb++) read_raw(0, kb);
+  read_scales(0);
 #pragma unroll
-  for (int k = 0; k < 4; k++)
+  for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-    for (int sl = 0; sl < 7; sl++) dq_slice(k, sl, 0);
-#pragma unroll
-  for (int k = 0; k < 4; k++) read_raw(1, k, 1);
-  read_scales(1, 1);
+    for (int sl = 0; sl < 7; sl++) dq_slice(kb, sl, 0);
   bv[0] = read_b(0, 0);
   bv[1] = read_b(0, 1);
   __builtin_amdgcn_sched_barrier(0);
@@ -381,25 +373,25 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
 #pragma unroll
   for (int rg = 0; rg < 4; rg++)
 #pragma unroll
-    for (int af = 0; af < 4; af++) asm volatile("" : "+a"(acc[rg][af]));
+    for (int hf = 0; hf < 2; hf++) asm volatile("" : "+a"(acc[rg][hf]));
 
   // ---- split-K hand-off: the partial tile goes to uncached scratch in register order
-  // ([tile][split][wave][rg][2c+hf][i][lane] float4s, 256 KiB per tile and split); the
+  // ([tile][split][wave][rg][hf][i][lane] float4s, 256 KiB per tile and split); the
   // last split to arrive at the tile's counter reads all splits back and adds them in
   // split order (so the result is bit-identical from run to run, whichever split comes
   // last), writes C and resets the counter.  Each thread's stores complete before the
   // workgroup barrier; the counter is bumped after it. ----
-  const float* const pbase = a.partial + ((size_t)tile * S) * 65536 + (size_t)w * 16384 + 4 * lane;
+  const float* const pbase = a.partial + ((size_t)tile * S) * 65536 + (size_t)w * 8192 + 4 * lane;
   if (S > 1) {
-    float* const pmine = a.partial + ((size_t)tile * S + z) * 65536 + (size_t)w * 16384 + 4 * lane;
+    float* const pmine = a.partial + ((size_t)tile * S + z) * 65536 + (size_t)w * 8192 + 4 * lane;
 #pragma unroll
     for (int rg = 0; rg < 4; rg++)
 #pragma unroll
-      for (int af = 0; af < 4; af++)
+      for (int hf = 0; hf < 2; hf++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
-          *reinterpret_cast<float4_t*>(pmine + ((rg * 4 + af) * 4 + i) * 256) =
-              (float4_t){acc[rg][af][4 * i], acc[rg][af][4 * i + 1], acc[rg][af][4 * i + 2], acc[rg][af][4 * i + 3]};
+          *reinterpret_cast<float4_t*>(pmine + ((rg * 2 + hf) * 4 + i) * 256) =
+              (float4_t){acc[rg][hf][4 * i], acc[rg][hf][4 * i + 1], acc[rg][hf][4 * i + 2], acc[rg][hf][4 * i + 3]};
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -410,33 +402,30 @@ __global__ __launch_bounds__(256, 1) void sm24_prefill_kernel(GemmArgs a) {
     if (arrived != (uint32_t)S) return;
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // accumulator float4 (rg, af, i) of this lane: registers, or the sum of the splits
-  auto result = [&](int rg, int af, int i) -> float4_t {
+  // accumulator float4 (rg, hf, i) of this lane: registers, or the sum of the splits
+  auto result = [&](int rg, int hf, int i) -> float4_t {
     if (S == 1)
-      return (float4_t){acc[rg][af][4 * i], acc[rg][af][4 * i + 1], acc[rg][af][4 * i + 2], acc[rg][af][4 * i + 3]};
+      return (float4_t){acc[rg][hf][4 * i], acc[rg][hf][4 * i + 1], acc[rg][hf][4 * i + 2], acc[rg][hf][4 * i + 3]};
     float4_t v = {0.f, 0.f, 0.f, 0.f};
-    const float* p = pbase + ((rg * 4 + af) * 4 + i) * 256;
+    const float* p = pbase + ((rg * 2 + hf) * 4 + i) * 256;
     for (int zz = 0; zz < S; zz++) v += *reinterpret_cast<const float4_t*>(p + (size_t)zz * 65536);
     return v;
   };
 
   // ---- epilogue: lane (rho, h) holds, for batch row m0 + 32rg + rho, the columns
-  // 64c' + 16q + 8h + 4hf + i (c' = cw + c) in register 4q + i of acc[rg][2c + hf]:
-  // eight consecutive columns per (rg, c, q) ----
+  // 64cw + 16q + 8h + 4hf + i in register 4q + i of acc[rg][hf]: eight consecutive
+  // columns per (rg, q) ----
 #pragma unroll
   for (int rg = 0; rg < 4; rg++) {
     const int m = m0 + 32 * rg + rho;
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int n = 64 * (cw + c) + 16 * q + 8 * h;
-        const float4_t v0 = result(rg, 2 * c, q), v1 = result(rg, 2 * c + 1, q);
-        half8_t o = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
-                     (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
-        if constexpr (!GROUPED) o = o * *reinterpret_cast<const half8_t*>(a.s + n);
-        if (m < M) *reinterpret_cast<half8_t*>(a.C + (size_t)m * N + n) = o;
-      }
+    for (int q = 0; q < 4; q++) {
+      const int n = 64 * cw + 16 * q + 8 * h;
+      const float4_t v0 = result(rg, 0, q), v1 = result(rg, 1, q);
+      half8_t o = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+                   (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+      if constexpr (!GROUPED) o = o * *reinterpret_cast<const half8_t*>(a.s + n);
+      if (m < M) *reinterpret_cast<half8_t*>(a.C + (size_t)m * N + n) = o;
     }
   }
 }

@@ -5,8 +5,8 @@ namespace sm24 {
 
 hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream) {
   const int tiles = (a.N / (64 * kPreChunks)) * ((a.M + kPreRows - 1) / kPreRows) * a.splits;
-  if (grouped) hipLaunchKernelGGL(sm24_prefill_kernel<true>, dim3(tiles), dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(sm24_prefill_kernel<false>, dim3(tiles), dim3(256), 0, stream, a);
+  if (grouped) hipLaunchKernelGGL(sm24_prefill_kernel<true>, dim3(tiles), dim3(kPreThreads), 0, stream, a);
+  else hipLaunchKernelGGL(sm24_prefill_kernel<false>, dim3(tiles), dim3(kPreThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -142,7 +142,7 @@ def test_prefill_smfmac_hazards(prefill_asm):
     kernels = _kernels(prefill_asm)
     assert len(kernels) == 2  # grouped and per-column scales
     for name, body in kernels.items():
-        assert sum(1 for l in body.split("\n") if "v_smfmac" in l) >= 128, name
+        assert sum(1 for l in body.split("\n") if "v_smfmac" in l) >= 64, name
         assert hazards(body) == [], name
 
 
@@ -150,5 +150,8 @@ def test_prefill_registers(prefill_asm):
     for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", prefill_asm, re.S):
         body = m.group(2)
         assert int(re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", body).group(1)) == 0, m.group(1)
-    # 256 accumulator registers in AGPRs, no VGPR<->AGPR copies in the k-loop
-    assert prefill_asm.count("; NumAgprs: 256") == 2
+    # 128 accumulator registers in AGPRs, and at most 128 VGPRs, so that two waves fit
+    # on a SIMD
+    assert prefill_asm.count("; NumAgprs: 128") == 2
+    for v in re.findall(r"; NumVgprs: (\d+)", prefill_asm):
+        assert int(v) <= 128
