@@ -10,7 +10,7 @@
 // duplicated or out of range alike), so the kernel issues as few load instructions
 // as the bytes allow and fills every lane with a distinct useful 16-byte piece.
 //
-// A stage covers KS k-blocks of the tile (KS * TC = 64 * NW column-k-blocks).  Its
+// A stage covers KS = NW * max(2, 64 / TC) k-blocks of the tile.  Its
 // pieces - packed values, metadata, scales and, for MB < 16, the activation rows -
 // form one list of P 16-byte pieces; thread t loads pieces t, t + NT, ... (SL slots)
 // of every stage, rows clamped to the operand, into a register ring D stages deep.
@@ -21,13 +21,19 @@
 // outputs are not stored); k-blocks past K read zero activations, so the last stage
 // needs no per-k-block branch.
 //
-// MFMA (v_smfmac_f32_16x16x32_f16) lane roles: lane (rho, h) = (l % 16, l / 16)
-// holds output column n0 + 16*cb + rho, dense groups 2h and 2h+1 of a k-block; its
-// activation operand is batch row rho, dense K 8h .. 8h+7 (16 contiguous bytes).
-// Group d of a column sits in word t = d mod 4 of the packed row, nibble pair
-// 2*blk + (d >= 4): lane group h reads words t0 = 2*(h&1), t0+1.  Wave w computes
-// k-blocks [w*KPW, (w+1)*KPW) of every stage for all column blocks; the waves'
-// partial sums are reduced in LDS at the end.
+// MFMA (v_smfmac_f32_16x16x64_f16, two k-blocks per instruction) lane roles: lane
+// (rho, h) = (l % 16, l / 16) holds output column n = n0 + 16*cb + rho, i.e. word j =
+// rho & 3 of column half blk = (rho >> 2) & 1 of 8-column group gl = rho >> 3, and
+// the MFMA groups 4h..4h+3 = real groups t0, t0+1, t0+4, t0+5 (t0 = 2*(h&1)) of
+// k-block h >> 1 of the pair.  Word t of a column holds groups t and t+4, so the
+// lane's 8 values are all four nibbles of column half blk in words t0 and t0+1
+// (bytes blk and blk+2): low nibbles give groups t0, t0+1, high nibbles t0+4, t0+5.
+// Its index is byte h&1 of the column's two metadata int16s (groups 0-3 and 4-7),
+// one v_perm of the 8-byte metadata unit.  Its activation operand is batch row rho,
+// real dense K 4*(t0 + 4*(h>>1)) .. +7 of each k-block of the pair (the same 16-byte
+// piece u = (h >> 1) | ((h & 1) << 1) of both k-block rows).  Wave w computes k-blocks
+// [w*KPW, (w+1)*KPW) of every stage for all column blocks; the waves' partial sums
+// are reduced in LDS at the end.
 #pragma once
 #include "sm24_device.h"
 
@@ -40,7 +46,7 @@ template <int TC, int NW, int MB, bool GROUPED, int VF, int MF>
 __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int NT = 64 * NW;                           // threads
   constexpr int NCB = TC / 16;                          // 16-column MFMA blocks per tile
-  constexpr int KPW = 64 / TC;                          // k-blocks per wave per stage
+  constexpr int KPW = cmax(2, 64 / TC);                 // k-blocks per wave per stage (pairs)
   constexpr int KS = KPW * NW;                          // k-blocks per stage
   constexpr int BPK = VF == VAL4 ? TC / 2 : 3 * TC / 8;  // 16-byte value pieces per k-block
   // 16-byte metadata pieces per k-block: the tile's 4*TC bytes of 4-bit metadata, or
@@ -63,7 +69,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // uses LDS buffer i & 1 (consecutive stages must alternate buffers, also across
   // the wrap from slot D-1 to slot 0).
   constexpr int LPS = SL + DA;
-  constexpr int RING_VGPRS = STAGED ? 48 : 80;
+  constexpr int RING_VGPRS = STAGED ? 40 : 64;
   constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
@@ -184,25 +190,28 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int gl = rho >> 3, blk = (rho >> 2) & 1, j = rho & 3;
   const int jb = j >> 1, jj = j & 1;
   const int t0 = 2 * (h & 1);
-  const int ehalf = h >> 1;                          // metadata int16: first/second 16 dense K
-  const uint32_t nsh = 4u * (2u * blk + ehalf);      // nibble-pair shift in a value word
-  const uint32_t msh = 8u * (h & 1);                 // index-byte shift in a metadata int16
+  const int kh = h >> 1;                             // k-block of the pair
+  const int au = kh | ((h & 1) << 1);                // activation piece of a k-block row
+  const uint32_t nsh = 8u * blk;                     // byte shift: column half in a value word
+  // metadata unit bytes -> index halfword: [byte h&1 of int16 blk, of int16 2 + blk]
+  const uint32_t msel = (uint32_t)(2 * blk + (h & 1)) | ((uint32_t)(4 + 2 * blk + (h & 1)) << 8) | 0x0c0c0000u;
   const int arow = rho & (MB - 1);                   // staged activation row (lanes rho < MB)
   // direct activation operand: batch row rho (rows past M repeat row M-1)
-  const _Float16* abase = a.A + (size_t)(rho < M ? rho : M - 1) * K + 8 * h;
+  const _Float16* abase = a.A + (size_t)(rho < M ? rho : M - 1) * K + 8 * au;
 
   // Per-lane LDS byte offsets of this wave's first k-block and column block; the
-  // k-block (q), column block (cb) and buffer parts are immediates.
+  // k-block pair (q2), column block (cb) and buffer parts are immediates.
   const int kw = wave * KPW;                          // first k-block of this wave in a stage
-  const uint32_t o_val = kw * (BPK * 16) + (VF == VAL4 ? 4 * (16 * gl + 4 * t0 + j) : 0);
+  const uint32_t o_val = (kw + kh) * (BPK * 16) + (VF == VAL4 ? 4 * (16 * gl + 4 * t0 + j) : 0);
   const int wi_lane = 16 * gl + 4 * t0 + j;           // 3-bit values: word index without cb
-  const uint32_t o_meta = MOFF + kw * (MPK * 16) + jb * 2 * TC + 8 * (2 * gl + jj) + 2 * (blk + 2 * ehalf);
-  const uint32_t o_mrow = MOFF + kw * (MPK * 16);
-  const uint32_t o_scale = SOFF + (kw >> 2) * 2 * TC + 2 * (8 * gl + 2 * j + blk);  // same group for all q
-  const uint32_t o_act = AOFF + (kw * MB + arow) * 64 + 16 * h;
+  const uint32_t o_meta = MOFF + (kw + kh) * (MPK * 16) + jb * 2 * TC + 8 * (2 * gl + jj);
+  const uint32_t o_mrow = MOFF + (kw + kh) * (MPK * 16);
+  const uint32_t o_scale = SOFF + (kw >> 2) * 2 * TC + 2 * (8 * gl + 2 * j + blk);  // same group for the wave
+  const uint32_t o_act = AOFF + (kw * MB + arow) * 64 + 16 * au;
   // Dequant constants held in VGPRs, so that mask-and-or is one v_and_or_b32.
-  uint32_t kMask, kMagic;
+  uint32_t kMask, kMaskHi, kMagic;
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
+  asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
 
   auto load_direct = [&](int s, int q) -> half8_t {
@@ -211,10 +220,11 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     return *reinterpret_cast<const half8_t*>(p);
   };
 
-  // one accumulator per k-block of a wave's share (no MFMA dependency chains)
-  float4_t acc[KPW][NCB];
+  // one accumulator per k-block pair of a wave's share (no MFMA dependency chains)
+  constexpr int KP = KPW / 2;
+  float4_t acc[KP][NCB];
 #pragma unroll
-  for (int q = 0; q < KPW; q++)
+  for (int q = 0; q < KP; q++)
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[q][cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
@@ -224,78 +234,94 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 
   auto compute = [&](const uint8_t* st, const half8_t* dact) {
 #pragma unroll
-    for (int q = 0; q < KPW; q++) {
-      half8_t act;
+    for (int q2 = 0; q2 < KP; q2++) {
+      half8_t act0, act1;
       if constexpr (STAGED) {
         // Only lanes of real batch rows read the staged row; the other lanes' MFMA
         // columns are never stored, so their operand keeps whatever the register
         // held (LDS reads are paid per active lane).
-        if (rho < MB) sact[q] = *reinterpret_cast<const half8_t*>(st + o_act + q * MB * 64);
-        act = sact[q];
+        if (rho < MB) {
+          sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
+          sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
+        }
+        act0 = sact[2 * q2];
+        act1 = sact[2 * q2 + 1];
       } else {
-        act = dact[q];
+        act0 = dact[2 * q2];
+        act1 = dact[2 * q2 + 1];
       }
+      const half16_t act = __builtin_shufflevector(act0, act1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;
         uint32_t w0, w1;
         if constexpr (VF == VAL4) {
-          // words t0 and t0+1 of the tile's k-block row
-          const uint8_t* vp = st + o_val + q * (BPK * 16) + 128 * cb;
+          // words t0 and t0+1 of the lane's k-block row
+          const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
           w0 = *reinterpret_cast<const uint32_t*>(vp);
           w1 = *reinterpret_cast<const uint32_t*>(vp + 16);
         } else {
-          const uint8_t* rowp = st + o_val + q * (BPK * 16);
+          const uint8_t* rowp = st + o_val + 2 * q2 * (BPK * 16);
           const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
           const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
           w0 = spread3(__builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3)) & 0xFFFFFFu);
           w1 = spread3(__builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3)) & 0xFFFFFFu);
         }
-        // values: nibble pairs of words t0, t0+1 -> {g_2h slot0, slot1, g_2h+1 slot0, slot1}
-        const uint32_t x0 = ((w0 >> nsh) & kMask) | kMagic;
-        const uint32_t x1 = ((w1 >> nsh) & kMask) | kMagic;
+        // values: bytes blk, blk+2 of words t0, t0+1; low nibbles -> groups t0, t0+1,
+        // high nibbles (16x) -> groups t0+4, t0+5, each {slot 0, slot 1}
+        const uint32_t x0 = w0 >> nsh, x1 = w1 >> nsh;
         constexpr float zp = VF == VAL4 ? 1032.0f : 1028.0f;  // 1024 + zero point
-        const half2_t v0 = __builtin_bit_cast(half2_t, x0) - (half2_t){(_Float16)zp, (_Float16)zp};
-        const half2_t v1 = __builtin_bit_cast(half2_t, x1) - (half2_t){(_Float16)zp, (_Float16)zp};
-        half4_t aop = (half4_t){v0.x, v0.y, v1.x, v1.y};
-        // metadata: int16 (blk, ehalf) of unit 16*jb + 2*gt + jj; byte h&1 holds the
-        // nibbles of dense groups 2h and 2h+1
+        constexpr float zh = (zp - 1024.0f) + 64.0f;          // the same for 1024 + 16 q, over 16
+        const half2_t kz = {(_Float16)zp, (_Float16)zp};
+        const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const half2_t kzh = {(_Float16)-zh, (_Float16)-zh};
+        const half2_t l0 = __builtin_bit_cast(half2_t, (x0 & kMask) | kMagic) - kz;
+        const half2_t l1 = __builtin_bit_cast(half2_t, (x1 & kMask) | kMagic) - kz;
+        const half2_t u0 = __builtin_bit_cast(half2_t, (x0 & kMaskHi) | kMagic) * k16 + kzh;
+        const half2_t u1 = __builtin_bit_cast(half2_t, (x1 & kMaskHi) | kMagic) * k16 + kzh;
+        half8_t aop = (half8_t){l0.x, l0.y, l1.x, l1.y, u0.x, u0.y, u1.x, u1.y};
+        // metadata: byte h&1 of int16s blk (groups 0-3) and 2 + blk (groups 4-7) of
+        // unit 16*jb + 2*gt + jj
         uint32_t idx;
         if constexpr (MF == META4) {
-          const uint16_t md = *reinterpret_cast<const uint16_t*>(st + o_meta + q * (MPK * 16) + 32 * cb);
-          idx = ((uint32_t)md >> msh) & 0xFFu;
+          const u32x2 unit = *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
+          idx = __builtin_amdgcn_perm(unit.y, unit.x, msel);
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
           // (jb = 0) or high 24 bits of field "first" (g < 4) or "second" (g >= 4)
           // at position P = u mod 16, built from words (which, which+1).
-          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + q * (MPK * 16));
-          uint32_t X, Y;
-          int which;
-          if constexpr (TC == 64) {
-            which = gt >> 2;
-            const int Pw = (4 * gt + 2 * jj + ehalf) & 15;
-            X = mrow[16 * which + Pw];
-            Y = mrow[16 * (which + 1) + Pw];
-          } else {
-            which = g0 >> 2;
-            const int pl = 4 * gt + 2 * jj + ehalf;
-            X = mrow[pl];
-            Y = mrow[TC / 2 + pl];
+          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + 2 * q2 * (MPK * 16));
+          idx = 0;
+#pragma unroll
+          for (int ehalf = 0; ehalf < 2; ehalf++) {
+            uint32_t X, Y;
+            int which;
+            if constexpr (TC == 64) {
+              which = gt >> 2;
+              const int Pw = (4 * gt + 2 * jj + ehalf) & 15;
+              X = mrow[16 * which + Pw];
+              Y = mrow[16 * (which + 1) + Pw];
+            } else {
+              which = g0 >> 2;
+              const int pl = 4 * gt + 2 * jj + ehalf;
+              X = mrow[pl];
+              Y = mrow[TC / 2 + pl];
+            }
+            uint32_t c24;
+            if (which == 0) c24 = jb ? ((X >> 24) | ((Y & 0xFFFFu) << 8)) : (X & 0xFFFFFFu);
+            else c24 = jb ? ((Y >> 8) & 0xFFFFFFu) : (((X >> 16) | (Y << 16)) & 0xFFFFFFu);
+            const uint32_t lut = jb ? kLutLow : kLutHigh;
+            const uint32_t pos = 3u * (4u * blk + 2u * (h & 1));  // nibbles 2(h&1), +1 of int16 blk
+            const uint32_t ca = (c24 >> pos) & 7u, cbv = (c24 >> (pos + 3u)) & 7u;
+            idx |= (((lut >> (4u * ca)) & 15u) | (((lut >> (4u * cbv)) & 15u) << 4)) << (8 * ehalf);
           }
-          uint32_t c24;
-          if (which == 0) c24 = jb ? ((X >> 24) | ((Y & 0xFFFFu) << 8)) : (X & 0xFFFFFFu);
-          else c24 = jb ? ((Y >> 8) & 0xFFFFFFu) : (((X >> 16) | (Y << 16)) & 0xFFFFFFu);
-          const uint32_t lut = jb ? kLutLow : kLutHigh;
-          const uint32_t pos = 3u * (4u * blk + 2u * (h & 1));  // nibbles 2(h&1), +1 of int16 blk
-          const uint32_t ca = (c24 >> pos) & 7u, cbv = (c24 >> (pos + 3u)) & 7u;
-          idx = ((lut >> (4u * ca)) & 15u) | (((lut >> (4u * cbv)) & 15u) << 4);
         }
         if constexpr (GROUPED) {
           const _Float16 sc = *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
-          aop = scale4(aop, sc);
+          aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
         }
-        acc[q][cb] = smfmac32<0>(aop, act, acc[q][cb], idx);
+        acc[q2][cb] = smfmac64<0>(aop, act, acc[q2][cb], idx);
       }
     }
   };
@@ -344,7 +370,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     if (base + i < nst) stage(i, false, base + i);  // uniform
 
 #pragma unroll
-  for (int q = 1; q < KPW; q++)
+  for (int q = 1; q < KP; q++)
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[0][cb] += acc[q][cb];
 
