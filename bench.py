@@ -92,9 +92,9 @@ class Call:
 
 def kernel_of(c) -> str:
     """The kernel the library dispatches a call to (the host rules of
-    csed499ii_amd/csrc/sm24_gemm.hip: decode for M <= 16, the prefill kernel for
+    csed499ii_amd/csrc/sm24_gemm.hip: decode for M <= 32, the prefill kernel for
     M >= 256 with 4-bit values and metadata, N % 512 == 0 and K % 128 == 0)."""
-    if c.M <= 16:
+    if c.M <= 32:
         return "sm24::sm24_decode_kernel"
     if c.M >= 256 and c.bits == 4 and c.meta_key == "meta" and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"

@@ -15,7 +15,8 @@
 // form one list of P 16-byte pieces; thread t loads pieces t, t + NT, ... (SL slots)
 // of every stage, rows clamped to the operand, into a register ring D stages deep.
 // When a stage is due its pieces are written to one of two LDS buffers and, after
-// one barrier, the NW waves read their MFMA operands from LDS.  For MB = 16 every
+// one barrier, the NW waves read their MFMA operands from LDS.  For MB = 16 (32: two
+// 16-row blocks, each weight fragment feeding two MFMAs) every
 // lane of the activation operand is a real batch row, so each wave loads its own
 // operands straight into the ring instead.  Batch rows past M read row M-1 (their
 // outputs are not stored); k-blocks past K read zero activations, so the last stage
@@ -54,13 +55,14 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int MPK = (MF == META3 && TC == 64) ? 12 : TC / 4;
   constexpr int SPG = TC / 8;                           // 16-byte scale pieces per scale group
   constexpr bool STAGED = MB < 16;                      // activations through LDS
+  constexpr int RB = MB > 16 ? MB / 16 : 1;             // 16-row batch blocks (MFMA B operands)
   constexpr int NB = KS * BPK;
   constexpr int NM = KS * MPK;
   constexpr int NSC = GROUPED ? (KS / 4) * SPG : 0;
   constexpr int NPA = STAGED ? KS * 4 * MB : 0;         // activation pieces (4 per row and k-block)
   constexpr int P1 = NB + NM, P2 = P1 + NSC, P = P2 + NPA;
   constexpr int SL = (P + NT - 1) / NT;                 // load slots per thread and stage
-  constexpr int DA = STAGED ? 0 : KPW;                  // direct activation loads per stage
+  constexpr int DA = STAGED ? 0 : KPW * RB;             // direct activation loads per stage
   constexpr int MOFF = NB * 16, SOFF = MOFF + NM * 16, AOFF = SOFF + NSC * 16;
   constexpr int STAGE = AOFF + NPA * 16;
   // Ring depth: at most ~56 loads in flight per wave (vmcnt counts to 63) and a
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // uses LDS buffer i & 1 (consecutive stages must alternate buffers, also across
   // the wrap from slot D-1 to slot 0).
   constexpr int LPS = SL + DA;
-  constexpr int RING_VGPRS = STAGED ? 40 : 64;
+  constexpr int RING_VGPRS = STAGED ? 40 : (RB > 1 || TC == 64 ? 48 : 64);
   constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
@@ -196,8 +198,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // metadata unit bytes -> index halfword: [byte h&1 of int16 blk, of int16 2 + blk]
   const uint32_t msel = (uint32_t)(2 * blk + (h & 1)) | ((uint32_t)(4 + 2 * blk + (h & 1)) << 8) | 0x0c0c0000u;
   const int arow = rho & (MB - 1);                   // staged activation row (lanes rho < MB)
-  // direct activation operand: batch row rho (rows past M repeat row M-1)
-  const _Float16* abase = a.A + (size_t)(rho < M ? rho : M - 1) * K + 8 * au;
+  // direct activation operands: batch rows rho + 16 rb (rows past M repeat row M-1)
+  const _Float16* abase[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int row = rho + 16 * rb;
+    abase[rb] = a.A + (size_t)(row < M ? row : M - 1) * K + 8 * au;
+  }
 
   // Per-lane LDS byte offsets of this wave's first k-block and column block; the
   // k-block pair (q2), column block (cb) and buffer parts are immediates.
@@ -214,19 +221,23 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
 
+  // direct load q = rb * KPW + (k-block of the wave's share)
   auto load_direct = [&](int s, int q) -> half8_t {
-    const int kb = s * KS + wave * KPW + q;  // uniform
-    const _Float16* p = kb < nkb ? abase + 32 * kb : a.zeros;
+    const int rb = q / KPW;
+    const int kb = s * KS + wave * KPW + q % KPW;  // uniform
+    const _Float16* p = kb < nkb ? abase[rb] + 32 * kb : a.zeros;
     return *reinterpret_cast<const half8_t*>(p);
   };
 
   // one accumulator per k-block pair of a wave's share (no MFMA dependency chains)
   constexpr int KP = KPW / 2;
-  float4_t acc[KP][NCB];
+  float4_t acc[KP][NCB][RB];
 #pragma unroll
   for (int q = 0; q < KP; q++)
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) acc[q][cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) acc[q][cb][rb] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
   half8_t sact[KPW];  // staged activation operands (lanes rho >= MB never reload)
 #pragma unroll
@@ -235,7 +246,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   auto compute = [&](const uint8_t* st, const half8_t* dact) {
 #pragma unroll
     for (int q2 = 0; q2 < KP; q2++) {
-      half8_t act0, act1;
+      half16_t act[RB];
       if constexpr (STAGED) {
         // Only lanes of real batch rows read the staged row; the other lanes' MFMA
         // columns are never stored, so their operand keeps whatever the register
@@ -244,13 +255,14 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
           sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
         }
-        act0 = sact[2 * q2];
-        act1 = sact[2 * q2 + 1];
+        act[0] = __builtin_shufflevector(sact[2 * q2], sact[2 * q2 + 1], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12,
+                                         13, 14, 15);
       } else {
-        act0 = dact[2 * q2];
-        act1 = dact[2 * q2 + 1];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+          act[rb] = __builtin_shufflevector(dact[rb * KPW + 2 * q2], dact[rb * KPW + 2 * q2 + 1], 0, 1, 2, 3, 4, 5, 6,
+                                            7, 8, 9, 10, 11, 12, 13, 14, 15);
       }
-      const half16_t act = __builtin_shufflevector(act0, act1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;
@@ -321,7 +333,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           const _Float16 sc = *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
           aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
         }
-        acc[q2][cb] = smfmac64<0>(aop, act, acc[q2][cb], idx);
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) acc[q2][cb][rb] = smfmac64<0>(aop, act[rb], acc[q2][cb][rb], idx);
       }
     }
   };
@@ -372,37 +385,44 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 #pragma unroll
   for (int q = 1; q < KP; q++)
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) acc[0][cb] += acc[q][cb];
+    for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) acc[0][cb][rb] += acc[q][cb][rb];
 
-  // ---- reduce the NW waves pairwise in LDS (fixed order); wave 0 writes C ----
+  // ---- reduce the NW waves pairwise in LDS (fixed order), one 16-row block at a
+  // time; wave 0 writes C ----
 #pragma unroll
-  for (int half = NW / 2; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
+  for (int rb = 0; rb < RB; rb++) {
 #pragma unroll
-      for (int cb = 0; cb < NCB; cb++)
+    for (int half = NW / 2; half >= 1; half >>= 1) {
+      if (wave >= half && wave < 2 * half) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) red[wave - half][rho][16 * cb + 4 * h + i] = acc[0][cb][i];
-    }
-    __syncthreads();
-    if (wave < half) {
+        for (int cb = 0; cb < NCB; cb++)
 #pragma unroll
-      for (int cb = 0; cb < NCB; cb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[0][cb][i] += red[wave][rho][16 * cb + 4 * h + i];
-    }
-    __syncthreads();
-  }
-  if (wave == 0 && rho < M) {
-#pragma unroll
-    for (int cb = 0; cb < NCB; cb++) {
-      const int n = n0 + 16 * cb + 4 * h;
-      half4_t o;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        o[i] = (_Float16)acc[0][cb][i];
-        if constexpr (!GROUPED) o[i] = o[i] * a.s[n + i];
+          for (int i = 0; i < 4; i++) red[wave - half][rho][16 * cb + 4 * h + i] = acc[0][cb][rb][i];
       }
-      *reinterpret_cast<half4_t*>(a.C + (size_t)rho * N + n) = o;
+      __syncthreads();
+      if (wave < half) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[0][cb][rb][i] += red[wave][rho][16 * cb + 4 * h + i];
+      }
+      __syncthreads();
+    }
+    const int row = rho + 16 * rb;
+    if (wave == 0 && row < M) {
+#pragma unroll
+      for (int cb = 0; cb < NCB; cb++) {
+        const int n = n0 + 16 * cb + 4 * h;
+        half4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          o[i] = (_Float16)acc[0][cb][rb][i];
+          if constexpr (!GROUPED) o[i] = o[i] * a.s[n + i];
+        }
+        *reinterpret_cast<half4_t*>(a.C + (size_t)row * N + n) = o;
+      }
     }
   }
 }

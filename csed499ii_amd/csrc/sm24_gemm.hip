@@ -457,11 +457,12 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 }
 
 // Column-tile width and waves per workgroup of the decode kernel, from measured
-// single-call times on MI355X (Llama-2-7B shapes, M in {1, 4, 8, 16}).  Tiles of
+// single-call times on MI355X (Llama-2-7B shapes, M in {1, 4, 8, 16, 24, 32}).  Tiles of
 // 16 columns give the most workgroups; wider tiles re-read the activation rows
 // fewer times, which pays once M > 1 and the grid still covers the CUs: 32-column
 // tiles when N/32 is at least twice the CU count, 64-column tiles when N/64 is at
-// least half of it.  MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES override.
+// least half of it (for M > 16, two batch blocks, whenever N/64 is).
+// MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES override.
 struct DecodeShape {
   int tc, nw;
 };
@@ -471,6 +472,7 @@ DecodeShape decode_shape(int M, int N, int cus) {
   DecodeShape d;
   const bool wide32 = N / 32 >= 2 * cus;
   if (M == 1) d = {wide32 ? 32 : 16, 8};
+  else if (M > 16) d = {2 * (N / 64) >= cus ? 64 : 16, 4};
   else if (wide32) d = {32, 4};
   else if (2 * (N / 64) >= cus) d = {64, 8};
   else d = {16, M <= 4 ? 8 : 4};
@@ -479,9 +481,9 @@ DecodeShape decode_shape(int M, int N, int cus) {
   return d;
 }
 
-// Padded batch of the decode kernel: 1, 4 (activations staged through LDS) or 16
-// (loaded straight into the MFMA operand).
-int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : 16); }
+// Padded batch of the decode kernel: 1, 4 (activations staged through LDS), 16 or 32
+// (loaded straight into the MFMA operands: one or two 16-row blocks).
+int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
 
 template <int TC, int NW, int MB, bool GROUPED>
 void launch_decode_mb(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
@@ -496,7 +498,8 @@ void launch_decode_nw(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
   const int mb = decode_batch(a.M);
   if (mb == 1) launch_decode_mb<TC, NW, 1, GROUPED>(a, vf, mf, stream);
   else if (mb == 4) launch_decode_mb<TC, NW, 4, GROUPED>(a, vf, mf, stream);
-  else launch_decode_mb<TC, NW, 16, GROUPED>(a, vf, mf, stream);
+  else if (mb == 16) launch_decode_mb<TC, NW, 16, GROUPED>(a, vf, mf, stream);
+  else launch_decode_mb<TC, NW, 32, GROUPED>(a, vf, mf, stream);
 }
 
 template <int TC, bool GROUPED>
@@ -579,7 +582,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       sms = 256;
   }
   const int M = prob_n, N = prob_m, K = prob_k;
-  if (M <= 16) {
+  if (M <= kDecodeMaxM) {
     // Decode: one workgroup per column tile over the whole K (no split-K).
     GemmArgs d{};
     d.A = static_cast<const _Float16*>(A);

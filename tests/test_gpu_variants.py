@@ -37,7 +37,7 @@ def test_meta3_rejects_invalid_nibbles():
 
 
 @pytest.mark.parametrize("M,N,K,g", [(1, 4096, 4096, 128), (16, 4096, 4096, 128), (48, 1024, 2048, -1),
-                                     (16, 12288, 4096, 128)])
+                                     (16, 12288, 4096, 128), (32, 4096, 4096, 128), (20, 12288, 4096, -1)])
 def test_meta3_gemm_equals_baseline_bit_exact(M, N, K, g):
     """Same arithmetic, compressed metadata: outputs must be identical."""
     wt = synth.make_weight(K, N, M + N, g, device=DEV)
@@ -53,7 +53,7 @@ def test_meta3_gemm_equals_baseline_bit_exact(M, N, K, g):
         assert_close(C1.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), "meta3")
 
 
-@pytest.mark.parametrize("M", [1, 16, 256])
+@pytest.mark.parametrize("M", [1, 16, 32, 256])
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 12288), (11008, 4096)])
 def test_w3_gemm_config4(M, K, N):
     """3-bit values, Llama-2-7B shapes, M in {1, 16, 256}."""
