@@ -363,6 +363,53 @@ int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** co
   return MARLIN_HIP_OK;
 }
 
+// Staging buffer for operands expanded to the large-M kernel's 4-bit formats (3-bit
+// values, 3-bit metadata), one per device and shared by every stream: calls that
+// overlap in time on one device must not both expand.  Ordinary device memory
+// (written and read by kernels of the same stream); grows, never freed.
+std::map<int, Scratch> g_stage;
+
+int get_stage(int dev, hipStream_t stream, size_t bytes, void** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  Scratch& s = g_stage[dev];
+  if (s.bytes < bytes) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone) {
+      set_error("marlin_hip: the operand staging buffer would have to grow during stream capture; make one "
+                "call of the same (or a larger) shape on this device before capturing");
+      return MARLIN_HIP_ERR_LAUNCH;
+    }
+    const size_t nb = bytes > 2 * s.bytes ? bytes : 2 * s.bytes;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, nb);
+    if (e != hipSuccess) {
+      set_error(std::string("marlin_hip: allocation of the staging buffer failed: ") + hipGetErrorString(e));
+      return MARLIN_HIP_ERR_LAUNCH;
+    }
+    s.ptr = p;
+    s.bytes = nb;
+  }
+  *out = s.ptr;
+  return MARLIN_HIP_OK;
+}
+
+// 3-bit value codes -> the 4-bit packed layout: 4-bit word w is the 24-bit field at
+// bit 24w of the 3-bit stream, each code spread to a nibble and offset by 4 (zero
+// point 4 -> 8), so (nibble - 8) * s equals (code - 4) * s.  One thread per 4 words
+// (12 bytes in, 16 out).
+__global__ __launch_bounds__(256) void w3_to_w4_kernel(const uint32_t* __restrict__ in, u32x4* __restrict__ out,
+                                                       long long quads) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= quads) return;
+  const uint32_t a0 = in[3 * i], a1 = in[3 * i + 1], a2 = in[3 * i + 2];
+  u32x4 o;
+  o.x = spread3(a0 & 0xFFFFFFu) + 0x44444444u;
+  o.y = spread3(__builtin_amdgcn_alignbit(a1, a0, 24) & 0xFFFFFFu) + 0x44444444u;
+  o.z = spread3(__builtin_amdgcn_alignbit(a2, a1, 16) & 0xFFFFFFu) + 0x44444444u;
+  o.w = spread3(a2 >> 8) + 0x44444444u;
+  out[i] = o;
+}
+
 // K splits of the large-M kernel.  Its workgroups fill the CUs one per CU, so a
 // problem with few tiles runs faster split along K when K is long enough to pay for
 // the hand-off: each split stores a 256 KiB fp32 partial to uncached scratch and the
@@ -606,6 +653,34 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       return MARLIN_HIP_ERR_LAUNCH;
     }
     return MARLIN_HIP_OK;
+  }
+  if (prefill_fits(M, N, K, VAL4, META4) && (vf != VAL4 || mf != META4)) {
+    // 3-bit values or metadata at large M: expand them into the 4-bit layouts on this
+    // stream, then the large-M kernel reads the expanded copy.
+    const size_t vbytes = vf == VAL3 ? (size_t)K * N / 4 : 0, mbytes = mf == META3 ? (size_t)K * N / 8 : 0;
+    void* stage = nullptr;
+    err = get_stage(dev, stream, vbytes + mbytes, &stage);
+    if (err != MARLIN_HIP_OK) {
+      if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+      return err;
+    }
+    if (vf == VAL3) {
+      const long long quads = (long long)K * N / 64;
+      hipLaunchKernelGGL(w3_to_w4_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                         static_cast<const uint32_t*>(B), static_cast<u32x4*>(stage), quads);
+      B = stage;
+    }
+    if (mf == META3) {
+      void* m4 = static_cast<char*>(stage) + vbytes;
+      err = marlin_hip_meta3_unpack(meta, m4, (long long)K * N / 8 / 4 * 3 / 4, dev, stream);
+      if (err != MARLIN_HIP_OK) {
+        if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+        return err;
+      }
+      meta = m4;
+    }
+    vf = VAL4;
+    mf = META4;
   }
   if (prefill_fits(M, N, K, vf, mf)) {
     GemmArgs p{};

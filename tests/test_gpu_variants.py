@@ -37,7 +37,8 @@ def test_meta3_rejects_invalid_nibbles():
 
 
 @pytest.mark.parametrize("M,N,K,g", [(1, 4096, 4096, 128), (16, 4096, 4096, 128), (48, 1024, 2048, -1),
-                                     (16, 12288, 4096, 128), (32, 4096, 4096, 128), (20, 12288, 4096, -1)])
+                                     (16, 12288, 4096, 128), (32, 4096, 4096, 128), (20, 12288, 4096, -1),
+                                     (300, 1024, 1024, 128), (512, 4096, 4096, -1)])
 def test_meta3_gemm_equals_baseline_bit_exact(M, N, K, g):
     """Same arithmetic, compressed metadata: outputs must be identical."""
     wt = synth.make_weight(K, N, M + N, g, device=DEV)
