@@ -43,7 +43,7 @@ namespace sm24 {
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-template <int TC, int NW, int MB, bool GROUPED, int VF, int MF>
+template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
 __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int NT = 64 * NW;                           // threads
   constexpr int NCB = TC / 16;                          // 16-column MFMA blocks per tile
@@ -71,7 +71,9 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // uses LDS buffer i & 1 (consecutive stages must alternate buffers, also across
   // the wrap from slot D-1 to slot 0).
   constexpr int LPS = SL + DA;
-  constexpr int RING_VGPRS = STAGED ? 40 : (RB > 1 || TC == 64 ? 48 : 64);
+  // DEEP: a ring as deep as the budget allows (long K: more bytes in flight per
+  // workgroup); otherwise 16 VGPRs, so that more workgroups are resident per CU.
+  constexpr int RING_VGPRS = !DEEP ? 16 : (STAGED ? 40 : (RB > 1 || TC == 64 ? 48 : 64));
   constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");

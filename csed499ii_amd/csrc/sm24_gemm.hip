@@ -504,12 +504,12 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 }
 
 // Column-tile width and waves per workgroup of the decode kernel, from measured
-// single-call times on MI355X (Llama-2-7B shapes, M in {1, 4, 8, 16, 24, 32}).  Tiles of
-// 16 columns give the most workgroups; wider tiles re-read the activation rows
-// fewer times, which pays once M > 1 and the grid still covers the CUs: 32-column
-// tiles when N/32 is at least twice the CU count, 64-column tiles when N/64 is at
-// least half of it (for M > 16, two batch blocks, whenever N/64 is).
-// MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES override.
+// single-call times on MI355X (Llama-2-7B shapes, M in {1, 2, 4, 8, 16, 24, 32}, every
+// forced choice).  Narrow N (fewer than CUs/2 64-column chunks) takes 16-column tiles
+// for enough workgroups; wider N takes 64-column tiles from M = 8 (the activation
+// rows are re-read by fewer tiles), and below that 32-column tiles when N/32 is at
+// least twice the CU count, else 16.  MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES
+// override.
 struct DecodeShape {
   int tc, nw;
 };
@@ -518,11 +518,12 @@ DecodeShape decode_shape(int M, int N, int cus) {
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   DecodeShape d;
   const bool wide32 = N / 32 >= 2 * cus;
-  if (M == 1) d = {wide32 ? 32 : 16, 8};
-  else if (M > 16) d = {2 * (N / 64) >= cus ? 64 : 16, 4};
-  else if (wide32) d = {32, 4};
-  else if (2 * (N / 64) >= cus) d = {64, 8};
-  else d = {16, M <= 4 ? 8 : 4};
+  const bool narrow = 2 * (N / 64) < cus;
+  if (M > 16) d = {narrow ? 16 : 64, 4};
+  else if (narrow) d = {16, M <= 4 ? 8 : 4};
+  else if (M >= 8) d = {64, wide32 ? 4 : 8};
+  else if (wide32) d = {32, M == 1 ? 4 : 8};
+  else d = {16, 4};
   if (forced_tc) d.tc = forced_tc;
   if (forced_nw) d.nw = forced_nw;
   return d;
@@ -535,9 +536,20 @@ int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32))
 template <int TC, int NW, int MB, bool GROUPED>
 void launch_decode_mb(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
   const dim3 grid(a.N / TC), block(64 * NW);
-  if (vf == VAL3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4>), grid, block, 0, stream, a);
-  else if (mf == META3) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META3>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META4>), grid, block, 0, stream, a);
+  // Register ring depth: deep for long K (one workgroup per CU streams more stages at
+  // once), shallow for K <= 8192 (more resident workgroups); measured on the
+  // Llama-2-7B shapes (K = 4096 and 11008).
+  const bool deep = a.K > 8192;
+  if (vf == VAL3) {
+    if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, false>), grid, block, 0, stream, a);
+  } else if (mf == META3) {
+    if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META3, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META3, false>), grid, block, 0, stream, a);
+  } else {
+    if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META4, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META4, false>), grid, block, 0, stream, a);
+  }
 }
 
 template <int TC, int NW, bool GROUPED>
