@@ -1,4 +1,4 @@
-// Decode-sized (M <= 16) 2:4 INT4 x FP16 GEMM for gfx950, no split-K.
+// Decode-sized (M <= 32) 2:4 INT4 x FP16 GEMM for gfx950, no split-K.
 //
 // One workgroup owns a tile of TC output columns (TC = 16, 32 or 64) over the whole
 // K, so the result never crosses workgroups: a cross-workgroup hand-off costs
@@ -78,8 +78,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2][STAGE];
-  __shared__ float red[NW / 2 > 0 ? NW / 2 : 1][16][TC + 1];
+  // Two stage buffers; after the last stage the same LDS holds every wave's partial
+  // tile (16 rows x TC columns of fp32, rows padded to TC + 4) for the reduction.
+  constexpr int REDP = TC + 4;
+  constexpr int REDB = NW * 16 * REDP * 4;
+  constexpr int LDSB = 2 * STAGE > REDB ? 2 * STAGE : REDB;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDSB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
   auto stage = [&](int i, bool reload, int s) {
-    uint8_t* st = lds[i & 1];
+    uint8_t* st = lds + (i & 1) * STAGE;
 #pragma unroll
     for (int q = 0; q < SL; q++) {
       if (slot_live(q)) {
@@ -391,36 +395,29 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 #pragma unroll
       for (int rb = 0; rb < RB; rb++) acc[0][cb][rb] += acc[q][cb][rb];
 
-  // ---- reduce the NW waves pairwise in LDS (fixed order), one 16-row block at a
-  // time; wave 0 writes C ----
+  // ---- reduce the NW waves in LDS, one 16-row block at a time: every wave stores its
+  // partial tile, then thread t < 4*TC adds the NW partials of 4 columns of one row in
+  // wave order (fixed, so results are deterministic) and writes them ----
+  float* const red = reinterpret_cast<float*>(lds);
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
+    __syncthreads();  // the last stage's (or the previous block's) LDS reads are done
 #pragma unroll
-    for (int half = NW / 2; half >= 1; half >>= 1) {
-      if (wave >= half && wave < 2 * half) {
+    for (int cb = 0; cb < NCB; cb++)
+      *reinterpret_cast<float4_t*>(red + (wave * 16 + rho) * REDP + 16 * cb + 4 * h) = acc[0][cb][rb];
+    __syncthreads();
+    if (tid < 4 * TC) {
+      const int r = tid / (TC / 4), c = 4 * (tid % (TC / 4));
+      float4_t v = *reinterpret_cast<const float4_t*>(red + r * REDP + c);
 #pragma unroll
-        for (int cb = 0; cb < NCB; cb++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) red[wave - half][rho][16 * cb + 4 * h + i] = acc[0][cb][rb][i];
-      }
-      __syncthreads();
-      if (wave < half) {
-#pragma unroll
-        for (int cb = 0; cb < NCB; cb++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) acc[0][cb][rb][i] += red[wave][rho][16 * cb + 4 * h + i];
-      }
-      __syncthreads();
-    }
-    const int row = rho + 16 * rb;
-    if (wave == 0 && row < M) {
-#pragma unroll
-      for (int cb = 0; cb < NCB; cb++) {
-        const int n = n0 + 16 * cb + 4 * h;
+      for (int w = 1; w < NW; w++) v += *reinterpret_cast<const float4_t*>(red + (w * 16 + r) * REDP + c);
+      const int row = r + 16 * rb;
+      if (row < M) {
+        const int n = n0 + c;
         half4_t o;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          o[i] = (_Float16)acc[0][cb][rb][i];
+          o[i] = (_Float16)v[i];
           if constexpr (!GROUPED) o[i] = o[i] * a.s[n + i];
         }
         *reinterpret_cast<half4_t*>(a.C + (size_t)row * N + n) = o;
