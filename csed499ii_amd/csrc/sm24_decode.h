@@ -272,32 +272,44 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;
-        uint32_t w0, w1;
+        // values: bytes blk, blk+2 of words t0, t0+1; low nibbles -> groups t0, t0+1,
+        // high nibbles (16x) -> groups t0+4, t0+5, each {slot 0, slot 1}; as halves
+        // 1024 + q (lo) and 1024 + 16q (hi) by the magic-number trick
+        uint32_t lo0, lo1, hi0, hi1;
         if constexpr (VF == VAL4) {
           // words t0 and t0+1 of the lane's k-block row
           const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
-          w0 = *reinterpret_cast<const uint32_t*>(vp);
-          w1 = *reinterpret_cast<const uint32_t*>(vp + 16);
+          const uint32_t x0 = *reinterpret_cast<const uint32_t*>(vp) >> nsh;
+          const uint32_t x1 = *reinterpret_cast<const uint32_t*>(vp + 16) >> nsh;
+          lo0 = (x0 & kMask) | kMagic;
+          lo1 = (x1 & kMask) | kMagic;
+          hi0 = (x0 & kMaskHi) | kMagic;
+          hi1 = (x1 & kMaskHi) | kMagic;
         } else {
+          // 3-bit codes: word w is the 24-bit field at byte 3w of the row, nibble p at
+          // bits 3p.  Shifted by 6 blk, the lane's four codes (nibbles 2blk, 2blk+1,
+          // 4+2blk, 5+2blk) sit at bits 0, 3, 12, 15 and go straight to the nibble
+          // positions 0, 4 (lo) and 16, 20 (hi) of the 4-bit path.
           const uint8_t* rowp = st + o_val + 2 * q2 * (BPK * 16);
           const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
           const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
-          w0 = spread3(__builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3)) & 0xFFFFFFu);
-          w1 = spread3(__builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3)) & 0xFFFFFFu);
+          const uint32_t y0 = __builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3) + 6 * blk);
+          const uint32_t y1 = __builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3) + 6 * blk);
+          lo0 = ((y0 & 0x7000u) << 4) | (y0 & 0x7u) | kMagic;
+          lo1 = ((y1 & 0x7000u) << 4) | (y1 & 0x7u) | kMagic;
+          hi0 = ((y0 & 0x38000u) << 5) | ((y0 & 0x38u) << 1) | kMagic;
+          hi1 = ((y1 & 0x38000u) << 5) | ((y1 & 0x38u) << 1) | kMagic;
         }
-        // values: bytes blk, blk+2 of words t0, t0+1; low nibbles -> groups t0, t0+1,
-        // high nibbles (16x) -> groups t0+4, t0+5, each {slot 0, slot 1}
-        const uint32_t x0 = w0 >> nsh, x1 = w1 >> nsh;
         constexpr float zp = VF == VAL4 ? 1032.0f : 1028.0f;  // 1024 + zero point
         constexpr float zh = (zp - 1024.0f) + 64.0f;          // the same for 1024 + 16 q, over 16
         const half2_t kz = {(_Float16)zp, (_Float16)zp};
         const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
         const half2_t kzh = {(_Float16)-zh, (_Float16)-zh};
-        const half2_t l0 = __builtin_bit_cast(half2_t, (x0 & kMask) | kMagic) - kz;
-        const half2_t l1 = __builtin_bit_cast(half2_t, (x1 & kMask) | kMagic) - kz;
-        const half2_t u0 = __builtin_bit_cast(half2_t, (x0 & kMaskHi) | kMagic) * k16 + kzh;
-        const half2_t u1 = __builtin_bit_cast(half2_t, (x1 & kMaskHi) | kMagic) * k16 + kzh;
+        const half2_t l0 = __builtin_bit_cast(half2_t, lo0) - kz;
+        const half2_t l1 = __builtin_bit_cast(half2_t, lo1) - kz;
+        const half2_t u0 = __builtin_bit_cast(half2_t, hi0) * k16 + kzh;
+        const half2_t u1 = __builtin_bit_cast(half2_t, hi1) * k16 + kzh;
         half8_t aop = (half8_t){l0.x, l0.y, l1.x, l1.y, u0.x, u0.y, u1.x, u1.y};
         // metadata: byte h&1 of int16s blk (groups 0-3) and 2 + blk (groups 4-7) of
         // unit 16*jb + 2*gt + jj
