@@ -100,3 +100,33 @@ def test_expand3_partial_blocks(groups):
     stream = rng.integers(0, 256, size=48 * groups, dtype=np.uint8)
     got = marlin.expand3(torch.from_numpy(stream).to(DEV))
     assert np.array_equal(got.cpu().numpy().view(np.uint32), o.expand3(stream))
+
+
+def _w3_as_w4(B3: torch.Tensor) -> torch.Tensor:
+    """The 4-bit packed words holding the same values as a 3-bit value stream: word w
+    is the 24-bit field at byte 3w, code p at bits 3p, moved to nibble p with the
+    zero point 4 -> 8 (restated on the CPU from the 3-bit layout, for this test)."""
+    b = B3.cpu().numpy().view(np.uint8).reshape(-1, 3).astype(np.uint32)
+    f = b[:, 0] | (b[:, 1] << 8) | (b[:, 2] << 16)
+    w = np.zeros_like(f)
+    for p in range(8):
+        w |= (((f >> (3 * p)) & 7) + 4) << (4 * p)
+    return torch.from_numpy(w.view(np.int32).copy()).to(DEV)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (16, 4096, 4096), (32, 1024, 8192), (256, 4096, 4096),
+                                   (300, 1024, 8192)])
+def test_w3_gemm_bit_exact_against_4bit_path(M, K, N):
+    """3-bit values give exactly the products of the same values packed at 4 bits
+    ((code - 4) * s == (nibble - 8) * s in fp16), on the decode kernel and on the
+    large-M path that expands them first: the outputs are bit-identical."""
+    wt = synth.make_weight(K, N, 7 + K + M, 128, bits=3, device=DEV)
+    A = synth.make_activation(M, K, 9, device=DEV)
+    B4 = _w3_as_w4(wt["B"])
+    C3 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    C4 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C3, wt["s"], _ws(N))
+    marlin.mul_2_4(A, B4, wt["meta"], C4, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    assert torch.isfinite(C3).all()
+    assert torch.equal(C3, C4)
