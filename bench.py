@@ -300,7 +300,8 @@ def main():
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         raise SystemExit("bench.py measures one GPU: the 2:4 GEMM has no multi-GPU path in this build "
-                         "(column sharding needs no communication; see DESIGN.md). Run with --gpus 1.")
+                         "(each GPU would own whole 64-column chunks of N, with no communication). "
+                         "Run with --gpus 1.")
     if not torch.cuda.is_available():
         raise SystemExit("no GPU visible")
     _lib.load()
