@@ -91,16 +91,23 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int N = a.N, K = a.K, M = a.M;
   const int nkb = K >> 5;
   const int ngroups = (nkb + 3) >> 2;
-  const int nst = (nkb + KS - 1) / KS;
+  // Split-K: block b = z * ntiles + tile; split z covers stages [st0, st1) of the tile
+  // (the host keeps splits <= the stage count).
+  const int ntiles = N / TC;
+  const int S = a.splits;
+  const int z = blockIdx.x / ntiles;
+  const int nst_all = (nkb + KS - 1) / KS;
+  const int st0 = (int)(((long long)nst_all * z) / S);
+  const int nst = (int)(((long long)nst_all * (z + 1)) / S) - st0;  // stages of this split
   // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8 XCDs
   // (block b runs on XCD b % 8) and each XCD has its own L2.  The SUB = 64/TC tiles of
   // one 64-column chunk share 128-byte lines of metadata and scales (a tile's packed
   // values are whole lines), so they go to blocks b = 8*(SUB*q + s) + x, which all
   // sit on XCD x: each line is fetched from HBM once instead of once per tile.
   constexpr int SUB = 64 / TC;
-  int tile = blockIdx.x;
+  int tile = blockIdx.x - z * ntiles;
   if constexpr (SUB > 1) {
-    if (gridDim.x % (8 * SUB) == 0) {
+    if (ntiles % (8 * SUB) == 0) {
       const int x = tile & 7, jx = tile >> 3;
       tile = (8 * (jx / SUB) + x) * SUB + jx % SUB;
     }
@@ -183,7 +190,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // a select on the loaded value would wait for the load right away).
   const uint8_t* zeros = reinterpret_cast<const uint8_t*>(a.zeros);
   auto load_slot = [&](int q, int s) -> u32x4 {
-    const uint32_t row = (uint32_t)s * sper[q] + srow0[q];
+    const uint32_t row = (uint32_t)(st0 + s) * sper[q] + srow0[q];
     const uint32_t r = row < srmax[q] ? row : srmax[q];
     const uint8_t* p = sbase[q] + (uint64_t)r * sstride[q];
     if (q * NT + NT > P2) {  // the slot may hold activation pieces
@@ -230,7 +237,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // direct load q = rb * KPW + (k-block of the wave's share)
   auto load_direct = [&](int s, int q) -> half8_t {
     const int rb = q / KPW;
-    const int kb = s * KS + wave * KPW + q % KPW;  // uniform
+    const int kb = (st0 + s) * KS + wave * KPW + q % KPW;  // uniform
     const _Float16* p = kb < nkb ? abase[rb] + 32 * kb : a.zeros;
     return *reinterpret_cast<const half8_t*>(p);
   };
@@ -409,8 +416,27 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 
   // ---- reduce the NW waves in LDS, one 16-row block at a time: every wave stores its
   // partial tile, then thread t < 4*TC adds the NW partials of 4 columns of one row in
-  // wave order (fixed, so results are deterministic) and writes them ----
+  // wave order (fixed, so results are deterministic) and writes them (to C, or with
+  // split-K to this split's fp32 partial in the uncached scratch) ----
   float* const red = reinterpret_cast<float*>(lds);
+  const int r_out = tid / (TC / 4), c_out = 4 * (tid % (TC / 4));  // for tid < 4*TC
+  auto write_c = [&](int rb, float4_t v) {
+    const int row = r_out + 16 * rb;
+    if (row < M) {
+      const int n = n0 + c_out;
+      half4_t o;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        o[i] = (_Float16)v[i];
+        if constexpr (!GROUPED) o[i] = o[i] * a.s[n + i];
+      }
+      *reinterpret_cast<half4_t*>(a.C + (size_t)row * N + n) = o;
+    }
+  };
+  // partial of (tile, split, rb): 16 x TC floats in row-major order
+  auto partial_at = [&](int zz, int rb) -> float* {
+    return a.partial + ((size_t)(tile * S + zz) * RB + rb) * (16 * TC) + r_out * TC + c_out;
+  };
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
     __syncthreads();  // the last stage's (or the previous block's) LDS reads are done
@@ -419,20 +445,33 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       *reinterpret_cast<float4_t*>(red + (wave * 16 + rho) * REDP + 16 * cb + 4 * h) = acc[0][cb][rb];
     __syncthreads();
     if (tid < 4 * TC) {
-      const int r = tid / (TC / 4), c = 4 * (tid % (TC / 4));
-      float4_t v = *reinterpret_cast<const float4_t*>(red + r * REDP + c);
+      float4_t v = *reinterpret_cast<const float4_t*>(red + r_out * REDP + c_out);
 #pragma unroll
-      for (int w = 1; w < NW; w++) v += *reinterpret_cast<const float4_t*>(red + (w * 16 + r) * REDP + c);
-      const int row = r + 16 * rb;
-      if (row < M) {
-        const int n = n0 + c;
-        half4_t o;
+      for (int w = 1; w < NW; w++) v += *reinterpret_cast<const float4_t*>(red + (w * 16 + r_out) * REDP + c_out);
+      if (S == 1) write_c(rb, v);
+      else *reinterpret_cast<float4_t*>(partial_at(z, rb)) = v;
+    }
+  }
+  if (S > 1) {
+    // hand-off: each thread's partial stores complete before the workgroup barrier;
+    // the tile's counter is bumped after it; the last split to arrive adds all splits'
+    // partials in split order (bit-identical whichever arrives last), writes C and
+    // resets the counter
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    __shared__ uint32_t arrived;
+    if (tid == 0) arrived = __hip_atomic_fetch_add(a.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    __syncthreads();
+    if (arrived != (uint32_t)S) return;
+    if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 4 * TC) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          o[i] = (_Float16)v[i];
-          if constexpr (!GROUPED) o[i] = o[i] * a.s[n + i];
-        }
-        *reinterpret_cast<half4_t*>(a.C + (size_t)row * N + n) = o;
+      for (int rb = 0; rb < RB; rb++) {
+        float4_t v = *reinterpret_cast<const float4_t*>(partial_at(0, rb));
+        for (int zz = 1; zz < S; zz++) v += *reinterpret_cast<const float4_t*>(partial_at(zz, rb));
+        write_c(rb, v);
       }
     }
   }

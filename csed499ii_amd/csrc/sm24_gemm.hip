@@ -529,17 +529,33 @@ DecodeShape decode_shape(int M, int N, int cus) {
   return d;
 }
 
+// K splits of the decode kernel: a workgroup per (column tile, split), the partial
+// tiles handed off through the uncached scratch (last split adds them in order).
+// The hand-off costs more than the extra workgroups gain except for wide N on
+// 64-column tiles from M = 8 (gate_up 4096x22016: 14.3 -> 12.6 us at M = 8, 14.9 ->
+// 13.9 at M = 16; qkv, o and down, measured at 1-3 splits, are slower split).
+// MARLIN_HIP_DECODE_SPLITS forces a count.
+int decode_splits(int M, int N, int K, DecodeShape d, int cus) {
+  static const int forced = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
+  const int kpw = 64 / d.tc > 2 ? 64 / d.tc : 2;
+  const int nst = (K / 32 + d.nw * kpw - 1) / (d.nw * kpw);
+  int s = forced ? forced : (d.tc == 64 && N / 64 >= cus && M >= 8 ? 2 : 1);
+  if (s > nst) s = nst;
+  if ((size_t)(N / d.tc) * sizeof(uint32_t) > kCounterBytes) s = 1;
+  return s;
+}
+
 // Padded batch of the decode kernel: 1, 4 (activations staged through LDS), 16 or 32
 // (loaded straight into the MFMA operands: one or two 16-row blocks).
 int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
 
 template <int TC, int NW, int MB, bool GROUPED>
 void launch_decode_mb(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
-  const dim3 grid(a.N / TC), block(64 * NW);
+  const dim3 grid(a.N / TC * a.splits), block(64 * NW);
   // Register ring depth: deep for long K (one workgroup per CU streams more stages at
   // once), shallow for K <= 8192 (more resident workgroups); measured on the
   // Llama-2-7B shapes (K = 4096 and 11008).
-  const bool deep = a.K > 8192;
+  const bool deep = a.K / a.splits > 8192;
   if (vf == VAL3) {
     if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, true>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, false>), grid, block, 0, stream, a);
@@ -656,13 +672,19 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
     d.M = M;
     d.N = N;
     d.K = K;
-    d.splits = 1;
+    const DecodeShape shape = decode_shape(M, N, sms);
+    d.splits = decode_splits(M, N, K, shape, sms);
     err = get_zeros(dev, &d.zeros);
+    if (err == MARLIN_HIP_OK && d.splits > 1) {
+      const int rows = decode_batch(M) > 16 ? decode_batch(M) : 16;
+      err = get_scratch(dev, stream, (size_t)(N / shape.tc) * d.splits * rows * shape.tc * sizeof(float), &d.counters,
+                        &d.partial);
+    }
     if (err != MARLIN_HIP_OK) {
       if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
       return err;
     }
-    hipError_t e = launch_decode(d, decode_shape(M, N, sms), vf, mf, groupsize != -1, stream);
+    hipError_t e = launch_decode(d, shape, vf, mf, groupsize != -1, stream);
     if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
     if (e != hipSuccess) {
       set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
