@@ -503,46 +503,52 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
   return fallback;
 }
 
-// Column-tile width and waves per workgroup of the decode kernel, from measured
-// single-call times on MI355X (Llama-2-7B shapes, M in {1, 2, 4, 8, 16, 24, 32}, every
-// forced choice).  Narrow N (fewer than CUs/2 64-column chunks) takes 16-column tiles
-// for enough workgroups; wider N takes 64-column tiles from M = 8 (the activation
-// rows are re-read by fewer tiles), and below that 32-column tiles when N/32 is at
-// least twice the CU count, else 16.  MARLIN_HIP_DECODE_TC / MARLIN_HIP_DECODE_WAVES
-// override.
+// Column-tile width, waves per workgroup and K splits of the decode kernel, from
+// measured single-call times on MI355X (Llama-2-7B shapes, M in {1, 2, 4, 8, 16, 24,
+// 32}, every forced choice).  Narrow N (fewer than CUs/2 64-column chunks) takes
+// 16-column tiles for enough workgroups, until M grows: every tile re-reads all M
+// activation rows over K, so from M = 8 (long K) or M > 16 wider tiles split along K
+// keep the workgroup count while cutting that traffic (down 11008x4096 at M = 32:
+// 23.4 -> 13.5 us).  Wider N takes 64-column tiles from M = 8, below that 32-column
+// tiles when N/32 is at least twice the CU count, else 16; from M = 8 its 64-column
+// tiles split K in two.  A split costs a hand-off through the uncached scratch
+// (>= 2.5 us), so it is used only where measured to pay.  MARLIN_HIP_DECODE_TC /
+// _WAVES / _SPLITS override.
 struct DecodeShape {
-  int tc, nw;
+  int tc, nw, splits;
 };
-DecodeShape decode_shape(int M, int N, int cus) {
+DecodeShape decode_shape(int M, int N, int K, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
+  static const int forced_splits = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
   DecodeShape d;
   const bool wide32 = N / 32 >= 2 * cus;
   const bool narrow = 2 * (N / 64) < cus;
-  if (M > 16) d = {narrow ? 16 : 64, 4};
-  else if (narrow) d = {16, M <= 4 ? 8 : 4};
-  else if (M >= 8) d = {64, wide32 ? 4 : 8};
-  else if (wide32) d = {32, M == 1 ? 4 : 8};
-  else d = {16, 4};
+  const bool longk = K >= 8192;
+  if (narrow) {
+    if (longk && M > 16) d = {64, 4, 4};
+    else if (longk && M > 8) d = {64, 8, 4};
+    else if (longk && M > 4) d = {32, 8, 2};
+    else if (M > 16) d = {32, 4, 2};
+    else d = {16, M <= 4 ? 8 : 4, 1};
+  } else if (M > 16) {
+    d = {64, 4, N / 64 >= cus ? 2 : 1};
+  } else if (M >= 8) {
+    d = {64, wide32 ? 4 : 8, N / 64 >= cus ? 2 : 1};
+  } else if (wide32) {
+    d = {32, M == 1 ? 4 : 8, 1};
+  } else {
+    d = {16, 4, 1};
+  }
   if (forced_tc) d.tc = forced_tc;
   if (forced_nw) d.nw = forced_nw;
-  return d;
-}
-
-// K splits of the decode kernel: a workgroup per (column tile, split), the partial
-// tiles handed off through the uncached scratch (last split adds them in order).
-// The hand-off costs more than the extra workgroups gain except for wide N on
-// 64-column tiles from M = 8 (gate_up 4096x22016: 14.3 -> 12.6 us at M = 8, 14.9 ->
-// 13.9 at M = 16; qkv, o and down, measured at 1-3 splits, are slower split).
-// MARLIN_HIP_DECODE_SPLITS forces a count.
-int decode_splits(int M, int N, int K, DecodeShape d, int cus) {
-  static const int forced = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
+  if (forced_splits) d.splits = forced_splits;
+  // at most one split per stage, and a counter per column tile
   const int kpw = 64 / d.tc > 2 ? 64 / d.tc : 2;
   const int nst = (K / 32 + d.nw * kpw - 1) / (d.nw * kpw);
-  int s = forced ? forced : (d.tc == 64 && N / 64 >= cus && M >= 8 ? 2 : 1);
-  if (s > nst) s = nst;
-  if ((size_t)(N / d.tc) * sizeof(uint32_t) > kCounterBytes) s = 1;
-  return s;
+  if (d.splits > nst) d.splits = nst;
+  if ((size_t)(N / d.tc) * sizeof(uint32_t) > kCounterBytes) d.splits = 1;
+  return d;
 }
 
 // Padded batch of the decode kernel: 1, 4 (activations staged through LDS), 16 or 32
@@ -672,8 +678,8 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
     d.M = M;
     d.N = N;
     d.K = K;
-    const DecodeShape shape = decode_shape(M, N, sms);
-    d.splits = decode_splits(M, N, K, shape, sms);
+    const DecodeShape shape = decode_shape(M, N, K, sms);
+    d.splits = shape.splits;
     err = get_zeros(dev, &d.zeros);
     if (err == MARLIN_HIP_OK && d.splits > 1) {
       const int rows = decode_batch(M) > 16 ? decode_batch(M) : 16;

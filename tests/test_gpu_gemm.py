@@ -112,7 +112,7 @@ def test_config1_and_decode_o_proj(M):
     _check(wt, A, _run(wt, A), f"4096^2 M={M}")
 
 
-@pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 22016), (11008, 4096)])
+@pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 22016), (11008, 4096), (4096, 4096)])
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 24, 32])
 def test_decode_sweep_full_size_slices(K, N, M):
     """Full-width calls (every decode tile width and padded batch), checked on
