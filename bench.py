@@ -92,14 +92,15 @@ class Call:
 
 def kernel_of(c) -> str:
     """The kernel the library dispatches a call to (the host rules of
-    csed499ii_amd/csrc/sm24_gemm.hip: decode for M <= 32; the prefill kernel, after
-    expanding 3-bit operands to 4 bits, for M >= 48 when N >= 8192 and M >= 160
-    otherwise, with N % 512 == 0 and K % 128 == 0; the general kernel between)."""
-    if c.M <= 32:
-        return "sm24::sm24_decode_kernel"
+    csed499ii_amd/csrc/sm24_gemm.hip: the prefill kernel, after expanding 3-bit
+    operands to 4 bits, for M >= 48 when N >= 8192 and M >= 160 otherwise, with
+    N % 512 == 0 and K % 128 == 0; else the decode kernel up to M = 96 (launches of
+    <= 32 rows); the general kernel beyond)."""
     min_m = 48 if c.N >= 8192 else 160
-    if c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
+    if c.M > 32 and c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"
+    if c.M <= 96:
+        return "sm24::sm24_decode_kernel"
     return "sm24::sm24_gemm_kernel"
 
 

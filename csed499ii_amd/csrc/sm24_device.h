@@ -115,7 +115,8 @@ struct GemmArgs {
 
 // Large-M kernel (sm24_prefill.hip): output columns per workgroup tile (N must be a
 // multiple) and its launcher.
-constexpr int kDecodeMaxM = 32;  // largest batch of the decode kernel (two 16-row blocks)
+constexpr int kDecodeMaxM = 32;       // largest batch of one decode launch (two 16-row blocks)
+constexpr int kDecodeChunkMaxM = 96;  // largest batch run as several decode launches
 constexpr int kPreTileCols = 512;
 constexpr size_t kPreSplitBytes = 512 * 128 * sizeof(float);  // fp32 partial of one tile
 hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream);
