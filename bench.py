@@ -93,10 +93,10 @@ class Call:
 def kernel_of(c) -> str:
     """The kernel the library dispatches a call to (the host rules of
     csed499ii_amd/csrc/sm24_gemm.hip: the prefill kernel, after expanding 3-bit
-    operands to 4 bits, for M >= 48 when N >= 8192 and M >= 160 otherwise, with
+    operands to 4 bits, for M >= 65 (N >= 16384), 97 (N >= 8192) or 160, with
     N % 512 == 0 and K % 128 == 0; else the decode kernel up to M = 96 (launches of
     <= 32 rows); the general kernel beyond)."""
-    min_m = 48 if c.N >= 8192 else 160
+    min_m = 65 if c.N >= 16384 else (97 if c.N >= 8192 else 160)
     if c.M > 32 and c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"
     if c.M <= 96:

@@ -602,18 +602,20 @@ hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool 
 }
 
 // Large-M path (sm24_prefill_kernel): 4-bit values and metadata, N a multiple of its
-// 512-column tile and K of its 64-deep k-step, for batches above the decode kernel's
-// from a threshold measured on MI355X (Llama-2-7B shapes, M in 48..384, against the
-// general kernel): M >= 48 when N >= 8192 (at least 16 column tiles), M >= 160 for
-// narrower N, where one 128-row tile per 512 columns leaves most CUs idle.
-// MARLIN_HIP_PREFILL_MIN_M (> 32) replaces the threshold.
+// 512-column tile and K of its 64-deep k-step, from a batch threshold measured on
+// MI355X (Llama-2-7B shapes, M in 48..384, against decode launches of <= 32 rows and
+// the general kernel).  Below ~128 rows one 128-row tile per 512 columns leaves most
+// CUs idle (a K = 4096 tile takes ~43 us on one CU), so decode launches win while
+// their count stays small: M >= 65 for N >= 16384 (gate_up at M = 96: 43.8 against
+// 57.9 us), M >= 97 for N >= 8192 (qkv at M = 96: 47.3 against 39.3 us), M >= 160 for
+// narrower N.  MARLIN_HIP_PREFILL_MIN_M (> 32) replaces the threshold.
 bool prefill_fits(int M, int N, int K, int vf, int mf) {
   static const int forced_min_m = [] {
     const char* e = getenv("MARLIN_HIP_PREFILL_MIN_M");
     const int x = e ? atoi(e) : 0;
     return x > kDecodeMaxM ? x : 0;
   }();
-  const int min_m = forced_min_m ? forced_min_m : (N >= 8192 ? 48 : 160);
+  const int min_m = forced_min_m ? forced_min_m : (N >= 16384 ? 65 : (N >= 8192 ? 97 : 160));
   return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 128 == 0 &&
          (long long)M * K < (1LL << 31) - 2048 && (long long)K * N < (1LL << 34);
 }

@@ -133,7 +133,7 @@ def test_decode_sweep_full_size_slices(K, N, M):
 @pytest.mark.parametrize("M,N,K,g", [(256, 512, 128, 128), (300, 1024, 256, -1), (257, 512, 192, -1),
                                      (257, 512, 384, -1), (320, 1024, 384, 128),
                                      (384, 1536, 512, 128), (640, 2048, 1024, 128),
-                                     (50, 8192, 1024, 128), (100, 8192, 512, -1), (160, 4096, 512, 128)])
+                                     (80, 16384, 512, 128), (100, 8192, 512, -1), (160, 4096, 512, 128)])
 def test_prefill_kernel_shapes(M, N, K, g):
     """The large-M kernel: ragged row tiles, 1-3 k-steps, per-column and grouped
     scales, several column tiles (every XCD ordering branch)."""
