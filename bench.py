@@ -1,6 +1,6 @@
 """Benchmark of the MI355X 2:4 INT4 x FP16 GEMM (libmarlin_hip.so).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill|w3|meta3|stack]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|decode70b|prefill|w3|meta3|stack]
 
 Default workload (BASELINE config "decode sweep"): Llama-2-7B projection shapes
 (K x N = 4096x12288 QKV, 4096x4096 O, 4096x22016 gate/up, 11008x4096 down) at batch
@@ -10,7 +10,8 @@ weights rotate through copies totalling more than the 256 MB Infinity Cache so e
 call streams its weight from HBM.  Prints ONE JSON line; ``value`` is the achieved
 HBM bandwidth on algorithmic compressed-weight bytes (25/64*K*N per call).
 
-Other workloads: ``prefill`` (Llama-2-70B shapes, M in {512..4096}, TFLOP/s),
+Other workloads: ``decode70b`` (the decode sweep on the Llama-2-70B shapes below),
+``prefill`` (Llama-2-70B shapes, M in {512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
 ``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}), ``copy`` (a plain
 1 GiB device copy: the calibration run for the HBM traffic counters).
@@ -212,8 +213,8 @@ def cpu_baseline(sample_shape=("o", 4096, 4096), Ms=(1, 16), reps=3):
 def build_workload(args, device):
     wl = args.workload
     calls = []
-    if wl in ("decode", "meta3", "w3"):
-        shapes = LLAMA7B
+    if wl in ("decode", "decode70b", "meta3", "w3"):
+        shapes = LLAMA70B if wl == "decode70b" else LLAMA7B
         Ms = [1, 2, 4, 8, 16] if wl != "w3" else [1, 16, 256]
         bits = 3 if wl == "w3" else 4
         weights = {}
@@ -228,8 +229,8 @@ def build_workload(args, device):
             for name, K, N in shapes:
                 A = synth.make_activation(M, K, synth.SEED_BASE + M, device=device)
                 calls.append(Call(name, K, N, M, weights[name], A, fn, meta_key))
-        cfg = {"workload": {"decode": "decode_sweep_llama2_7b", "meta3": "decode_sweep_llama2_7b_meta3",
-                            "w3": "w3_values_llama2_7b"}[wl],
+        cfg = {"workload": {"decode": "decode_sweep_llama2_7b", "decode70b": "decode_sweep_llama2_70b",
+                            "meta3": "decode_sweep_llama2_7b_meta3", "w3": "w3_values_llama2_7b"}[wl],
                "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in shapes], "groupsize": 128,
                "weight_copies": copies,
                "rotated_weight_bytes": {n: copies[n] * synth.weight_bytes(K, N, bits, 128) for n, K, N in shapes}}
@@ -293,7 +294,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode", "prefill", "w3", "meta3", "stack", "copy"])
+    p.add_argument("--workload", default="decode", choices=["decode", "decode70b", "prefill", "w3", "meta3", "stack", "copy"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -364,9 +365,9 @@ def main():
         log("bench: per-call timing")
         pcs = per_call_stats(calls if args.workload != "stack" else calls[:4])
         out["per_call"] = pcs
-    if not args.no_cpu_baseline and args.workload in ("decode", "meta3", "w3", "stack"):
+    if not args.no_cpu_baseline and args.workload in ("decode", "decode70b", "meta3", "w3", "stack"):
         log("bench: cpu baseline (oracle)")
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(("o", 8192, 8192) if args.workload == "decode70b" else ("o", 4096, 4096))
     elif not args.no_cpu_baseline:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -504,23 +504,27 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 }
 
 // Column-tile width, waves per workgroup and K splits of the decode kernel, from
-// measured single-call times on MI355X (Llama-2-7B shapes, M in {1, 2, 4, 8, 16, 24,
-// 32}, every forced choice).  Narrow N (fewer than CUs/2 64-column chunks) takes
+// measured single-call times on MI355X (Llama-2-7B and -70B shapes, M in {1, 2, 4, 8,
+// 16, 24, 32}, every forced choice).  Narrow N (fewer than CUs/2 64-column chunks) takes
 // 16-column tiles for enough workgroups, until M grows: every tile re-reads all M
 // activation rows over K, so from M = 8 (long K) or M > 16 wider tiles split along K
 // keep the workgroup count while cutting that traffic (down 11008x4096 at M = 32:
 // 23.4 -> 13.5 us).  Wider N takes 64-column tiles from M = 8, below that 32-column
 // tiles when N/32 is at least twice the CU count, else 16; from M = 8 its 64-column
 // tiles split K in two.  A split costs a hand-off through the uncached scratch
-// (>= 2.5 us), so it is used only where measured to pay.  MARLIN_HIP_DECODE_TC /
-// _WAVES / _SPLITS override.
+// (>= 2.5 us), so it is used only where measured to pay.  Long K (>= 8192) at wider
+// N splits K four ways at N <= 10240 (Llama-2-70B qkv, o, down: 707 -> 589 us over
+// M in {1..32}, within 1.4 % of the best forced choice per call).
+// MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
 struct DecodeShape {
   int tc, nw, splits;
+  bool deep;  // register ring: deep (more stages in flight) or 16 VGPRs
 };
 DecodeShape decode_shape(int M, int N, int K, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   static const int forced_splits = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
+  static const int forced_deep = env_choice("MARLIN_HIP_DECODE_DEEP", {0, 1}, -1);
   DecodeShape d;
   const bool wide32 = N / 32 >= 2 * cus;
   const bool narrow = 2 * (N / 64) < cus;
@@ -531,6 +535,14 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
     else if (longk && M > 4) d = {32, 8, 2};
     else if (M > 16) d = {32, 4, 2};
     else d = {16, M <= 4 ? 8 : 4, 1};
+  } else if (longk) {
+    // long K at wide N (the Llama-2-70B shapes): K splits of 64-column tiles; 16- or
+    // 32-column tiles for few rows where N/16 fills one round of two per CU.
+    if (wide32) d = {64, 4, M > 8 ? 2 : 1};
+    else if (M > 8) d = {64, 4, 4};
+    else if (K >= 16384) d = {64, 8, 4};
+    else if (N / 16 <= 2 * cus) d = {M <= 4 ? 16 : 32, 8, 1};
+    else d = {M <= 4 ? 32 : 64, 4, 4};
   } else if (M > 16) {
     d = {64, 4, N / 64 >= cus ? 2 : 1};
   } else if (M >= 8) {
@@ -548,6 +560,10 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   const int nst = (K / 32 + d.nw * kpw - 1) / (d.nw * kpw);
   if (d.splits > nst) d.splits = nst;
   if ((size_t)(N / d.tc) * sizeof(uint32_t) > kCounterBytes) d.splits = 1;
+  // Register ring depth: deep for long K per split (one workgroup per CU streams more
+  // stages at once), shallow for K <= 8192 (more resident workgroups); measured on
+  // the Llama-2-7B shapes (K = 4096 and 11008).
+  d.deep = forced_deep >= 0 ? forced_deep == 1 : K / d.splits > 8192;
   return d;
 }
 
@@ -556,12 +572,8 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
 int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
 
 template <int TC, int NW, int MB, bool GROUPED>
-void launch_decode_mb(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
+void launch_decode_mb(const GemmArgs& a, bool deep, int vf, int mf, hipStream_t stream) {
   const dim3 grid(a.N / TC * a.splits), block(64 * NW);
-  // Register ring depth: deep for long K (one workgroup per CU streams more stages at
-  // once), shallow for K <= 8192 (more resident workgroups); measured on the
-  // Llama-2-7B shapes (K = 4096 and 11008).
-  const bool deep = a.K / a.splits > 8192;
   if (vf == VAL3) {
     if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, true>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, false>), grid, block, 0, stream, a);
@@ -575,30 +587,30 @@ void launch_decode_mb(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
 }
 
 template <int TC, int NW, bool GROUPED>
-void launch_decode_nw(const GemmArgs& a, int vf, int mf, hipStream_t stream) {
+void launch_decode_nw(const GemmArgs& a, bool deep, int vf, int mf, hipStream_t stream) {
   const int mb = decode_batch(a.M);
-  if (mb == 1) launch_decode_mb<TC, NW, 1, GROUPED>(a, vf, mf, stream);
-  else if (mb == 4) launch_decode_mb<TC, NW, 4, GROUPED>(a, vf, mf, stream);
-  else if (mb == 16) launch_decode_mb<TC, NW, 16, GROUPED>(a, vf, mf, stream);
-  else launch_decode_mb<TC, NW, 32, GROUPED>(a, vf, mf, stream);
+  if (mb == 1) launch_decode_mb<TC, NW, 1, GROUPED>(a, deep, vf, mf, stream);
+  else if (mb == 4) launch_decode_mb<TC, NW, 4, GROUPED>(a, deep, vf, mf, stream);
+  else if (mb == 16) launch_decode_mb<TC, NW, 16, GROUPED>(a, deep, vf, mf, stream);
+  else launch_decode_mb<TC, NW, 32, GROUPED>(a, deep, vf, mf, stream);
 }
 
 template <int TC, bool GROUPED>
-hipError_t launch_decode_t(const GemmArgs& a, int nw, int vf, int mf, hipStream_t stream) {
-  if (nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, vf, mf, stream);
-  else launch_decode_nw<TC, 8, GROUPED>(a, vf, mf, stream);
+hipError_t launch_decode_t(const GemmArgs& a, const DecodeShape& d, int vf, int mf, hipStream_t stream) {
+  if (d.nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, d.deep, vf, mf, stream);
+  else launch_decode_nw<TC, 8, GROUPED>(a, d.deep, vf, mf, stream);
   return hipGetLastError();
 }
 
 hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool grouped, hipStream_t stream) {
   if (grouped) {
-    if (d.tc == 64) return launch_decode_t<64, true>(a, d.nw, vf, mf, stream);
-    if (d.tc == 32) return launch_decode_t<32, true>(a, d.nw, vf, mf, stream);
-    return launch_decode_t<16, true>(a, d.nw, vf, mf, stream);
+    if (d.tc == 64) return launch_decode_t<64, true>(a, d, vf, mf, stream);
+    if (d.tc == 32) return launch_decode_t<32, true>(a, d, vf, mf, stream);
+    return launch_decode_t<16, true>(a, d, vf, mf, stream);
   }
-  if (d.tc == 64) return launch_decode_t<64, false>(a, d.nw, vf, mf, stream);
-  if (d.tc == 32) return launch_decode_t<32, false>(a, d.nw, vf, mf, stream);
-  return launch_decode_t<16, false>(a, d.nw, vf, mf, stream);
+  if (d.tc == 64) return launch_decode_t<64, false>(a, d, vf, mf, stream);
+  if (d.tc == 32) return launch_decode_t<32, false>(a, d, vf, mf, stream);
+  return launch_decode_t<16, false>(a, d, vf, mf, stream);
 }
 
 // Large-M path (sm24_prefill_kernel): 4-bit values and metadata, N a multiple of its

@@ -130,6 +130,35 @@ def test_decode_sweep_full_size_slices(K, N, M):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"{K}x{N} M={M} slice {c0}")
 
 
+_W70 = {}
+
+
+def _weight70(K, N):
+    """One Llama-2-70B weight at a time (device and host copies), reused across M."""
+    if (K, N) not in _W70:
+        _W70.clear()
+        wt = synth.make_weight(K, N, K + N, 128, device=DEV)
+        _W70[(K, N)] = (wt, to_cpu(wt))
+    return _W70[(K, N)]
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (28672, 8192), (8192, 57344)])
+def test_decode_llama70b_full_size_slices(K, N, M):
+    """The Llama-2-70B decode shapes (long K: 16-, 32- and 64-column tiles, K split
+    four ways), checked on column slices; repeated calls must be bit-identical."""
+    wt, t = _weight70(K, N)
+    A = synth.make_activation(M, K, 70 + M, device=DEV)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    for _ in range(2):
+        assert torch.equal(_run(wt, A), C), "repeated decode calls differ"
+    chunks = N // 64
+    for c0 in (0, chunks // 2 - 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"{K}x{N} M={M} slice {c0}")
+
+
 @pytest.mark.parametrize("M,N,K,g", [(256, 512, 128, 128), (300, 1024, 256, -1), (257, 512, 192, -1),
                                      (257, 512, 384, -1), (320, 1024, 384, 128),
                                      (384, 1536, 512, 128), (640, 2048, 1024, 128),
