@@ -97,7 +97,7 @@ def kernel_of(c) -> str:
     operands to 4 bits, for M >= 65 (N >= 16384), 97 (N >= 8192) or 160, with
     N % 512 == 0 and K % 128 == 0; else the decode kernel up to M = 96 (launches of
     <= 32 rows); the general kernel beyond)."""
-    min_m = 65 if c.N >= 16384 else (97 if c.N >= 8192 else 160)
+    min_m = 65 if c.N >= 16384 else (97 if c.N >= 4096 else 160)
     if c.M > 32 and c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"
     if c.M <= 96:

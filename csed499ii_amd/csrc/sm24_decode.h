@@ -467,12 +467,24 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     if (arrived != (uint32_t)S) return;
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < 4 * TC) {
+      // up to four splits' partials per batch of loads (the uncached reads are
+      // latency-bound: one wait per batch, not per split)
+      float4_t v[RB];
+      for (int z0 = 0; z0 < S; z0 += 4) {
+        float4_t t[RB][4];
 #pragma unroll
-      for (int rb = 0; rb < RB; rb++) {
-        float4_t v = *reinterpret_cast<const float4_t*>(partial_at(0, rb));
-        for (int zz = 1; zz < S; zz++) v += *reinterpret_cast<const float4_t*>(partial_at(zz, rb));
-        write_c(rb, v);
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            if (z0 + i < S) t[rb][i] = *reinterpret_cast<const float4_t*>(partial_at(z0 + i, rb));
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            if (z0 + i < S) v[rb] = z0 + i == 0 ? t[rb][0] : v[rb] + t[rb][i];
       }
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) write_c(rb, v[rb]);
     }
   }
 }

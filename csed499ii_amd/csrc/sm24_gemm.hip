@@ -414,8 +414,9 @@ __global__ __launch_bounds__(256) void w3_to_w4_kernel(const uint32_t* __restric
 // problem with few tiles runs faster split along K when K is long enough to pay for
 // the hand-off: each split stores a 256 KiB fp32 partial to uncached scratch and the
 // last one reads them all back.  The estimate is rounds x (k-steps per split) plus
-// that traffic, at the rates measured on MI355X (0.67 us per k-step of a tile, ~1.4
-// TB/s for the exchange).  MARLIN_HIP_PREFILL_SPLITS forces a count (read once).
+// that traffic, at the rates measured on MI355X (0.67 us per k-step of a tile, ~2.5
+// TB/s for the exchange: forced splits 2-4 on the Llama-2-7B and -70B shapes at M =
+// 128..1024).  MARLIN_HIP_PREFILL_SPLITS forces a count (read once).
 int prefill_splits(int tiles, int nks, int cus) {
   static const int forced = [] {
     const char* e = getenv("MARLIN_HIP_PREFILL_SPLITS");
@@ -424,7 +425,7 @@ int prefill_splits(int tiles, int nks, int cus) {
   }();
   const int max_s = nks / 8;  // at least eight k-steps per split
   if (forced) return forced < max_s ? forced : (max_s > 0 ? max_s : 1);
-  const double step_us = 0.67, exchange_bytes_per_us = 1.4e6;
+  const double step_us = 0.67, exchange_bytes_per_us = 2.5e6;
   int best_s = 1;
   double best = 1e30;
   for (int s = 1; s <= 8 && s <= max_s; s++) {
@@ -617,17 +618,19 @@ hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool 
 // 512-column tile and K of its 64-deep k-step, from a batch threshold measured on
 // MI355X (Llama-2-7B shapes, M in 48..384, against decode launches of <= 32 rows and
 // the general kernel).  Below ~128 rows one 128-row tile per 512 columns leaves most
-// CUs idle (a K = 4096 tile takes ~43 us on one CU), so decode launches win while
-// their count stays small: M >= 65 for N >= 16384 (gate_up at M = 96: 43.8 against
-// 57.9 us), M >= 97 for N >= 8192 (qkv at M = 96: 47.3 against 39.3 us), M >= 160 for
-// narrower N.  MARLIN_HIP_PREFILL_MIN_M (> 32) replaces the threshold.
+// CUs idle and the planner splits K, so decode launches win while their count stays
+// small: M >= 65 for N >= 16384 (gate_up at M = 96: 43.8 against 57.9 us), M >= 97
+// for N >= 4096 (qkv at M = 96: 34.3 against 35.6 us; down at M = 96: 43.5 against
+// 35.3; at M = 144 o takes 33.3 against 44.9 us on the general kernel, down 46.4
+// against 80.4), M >= 160 for narrower N.  MARLIN_HIP_PREFILL_MIN_M (> 32) replaces
+// the threshold.
 bool prefill_fits(int M, int N, int K, int vf, int mf) {
   static const int forced_min_m = [] {
     const char* e = getenv("MARLIN_HIP_PREFILL_MIN_M");
     const int x = e ? atoi(e) : 0;
     return x > kDecodeMaxM ? x : 0;
   }();
-  const int min_m = forced_min_m ? forced_min_m : (N >= 16384 ? 65 : (N >= 8192 ? 97 : 160));
+  const int min_m = forced_min_m ? forced_min_m : (N >= 16384 ? 65 : (N >= 4096 ? 97 : 160));
   return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 128 == 0 &&
          (long long)M * K < (1LL << 31) - 2048 && (long long)K * N < (1LL << 34);
 }

@@ -385,13 +385,15 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   if (S > 1) {
     float* const pmine = a.partial + ((size_t)tile * S + z) * 65536 + (size_t)w * 8192 + 4 * lane;
 #pragma unroll
-    for (int rg = 0; rg < 4; rg++)
+    for (int rg = 0; rg < 4; rg++) {
+      if (m0 + 32 * rg >= M) break;  // 32-row blocks past M are never read back (uniform)
 #pragma unroll
       for (int hf = 0; hf < 2; hf++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
           *reinterpret_cast<float4_t*>(pmine + ((rg * 2 + hf) * 4 + i) * 256) =
               (float4_t){acc[rg][hf][4 * i], acc[rg][hf][4 * i + 1], acc[rg][hf][4 * i + 2], acc[rg][hf][4 * i + 3]};
+    }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -402,26 +404,49 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
     if (arrived != (uint32_t)S) return;
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // accumulator float4 (rg, hf, i) of this lane: registers, or the sum of the splits
-  auto result = [&](int rg, int hf, int i) -> float4_t {
-    if (S == 1)
-      return (float4_t){acc[rg][hf][4 * i], acc[rg][hf][4 * i + 1], acc[rg][hf][4 * i + 2], acc[rg][hf][4 * i + 3]};
-    float4_t v = {0.f, 0.f, 0.f, 0.f};
-    const float* p = pbase + ((rg * 2 + hf) * 4 + i) * 256;
-    for (int zz = 0; zz < S; zz++) v += *reinterpret_cast<const float4_t*>(p + (size_t)zz * 65536);
-    return v;
-  };
-
   // ---- epilogue: lane (rho, h) holds, for batch row m0 + 32rg + rho, the columns
   // 64cw + 16q + 8h + 4hf + i in register 4q + i of acc[rg][hf]: eight consecutive
-  // columns per (rg, q) ----
+  // columns per (rg, q).  With split-K the float4 (hf, q) of the sum is read back
+  // from every split, in split order, two splits' 8 float4s per batch of loads: the
+  // uncached reads are latency-bound, so each batch keeps 16 loads in flight. ----
 #pragma unroll
   for (int rg = 0; rg < 4; rg++) {
+    if (m0 + 32 * rg >= M) break;  // uniform: no rows of this block are stored
+    float4_t v[2][4];
+    if (S == 1) {
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          v[hf][q] = (float4_t){acc[rg][hf][4 * q], acc[rg][hf][4 * q + 1], acc[rg][hf][4 * q + 2],
+                                acc[rg][hf][4 * q + 3]};
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k >> 2][k & 3] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      const float* p = pbase + rg * 8 * 256;
+      for (int zz = 0; zz < S; zz += 2) {
+        const bool two = zz + 1 < S;  // uniform
+        float4_t t0[8], t1[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) t0[k] = *reinterpret_cast<const float4_t*>(p + k * 256 + (size_t)zz * 65536);
+        if (two) {
+#pragma unroll
+          for (int k = 0; k < 8; k++)
+            t1[k] = *reinterpret_cast<const float4_t*>(p + k * 256 + (size_t)(zz + 1) * 65536);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k >> 2][k & 3] += t0[k];
+        if (two) {
+#pragma unroll
+          for (int k = 0; k < 8; k++) v[k >> 2][k & 3] += t1[k];
+        }
+      }
+    }
     const int m = m0 + 32 * rg + rho;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int n = 64 * cw + 16 * q + 8 * h;
-      const float4_t v0 = result(rg, 0, q), v1 = result(rg, 1, q);
+      const float4_t v0 = v[0][q], v1 = v[1][q];
       half8_t o = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
                    (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
       if constexpr (!GROUPED) o = o * *reinterpret_cast<const half8_t*>(a.s + n);

@@ -172,7 +172,8 @@ def test_prefill_kernel_shapes(M, N, K, g):
     assert torch.equal(_run(wt, A), C), "repeated calls differ"
 
 
-@pytest.mark.parametrize("M,N,K,g", [(300, 512, 8192, -1), (1000, 2048, 8192, 128), (256, 1024, 4096, 128)])
+@pytest.mark.parametrize("M,N,K,g", [(300, 512, 8192, -1), (1000, 2048, 8192, 128), (256, 1024, 4096, 128),
+                                     (100, 4096, 4096, 128), (130, 4096, 11008, -1)])
 def test_prefill_split_k(M, N, K, g):
     """Large-M kernel split along K (few tiles, long K: the planner picks 3-7 splits):
     partials handed off through the scratch, reduced by the last split in split order,
