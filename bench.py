@@ -14,7 +14,8 @@ Other workloads: ``decode70b`` (the decode sweep on the Llama-2-70B shapes below
 ``prefill`` (Llama-2-70B shapes, M in {512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
 ``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}), ``copy`` (a plain
-1 GiB device copy: the calibration run for the HBM traffic counters).
+1 GiB device copy: the calibration run for the HBM traffic counters), ``compare``
+(per call site against hipBLASLt dense fp16 and hipSPARSELt 2:4 fp16).
 
 ``roofline.traffic`` is read from ``profiles/<workload>_hbm_traffic.md`` (HBM
 bytes per launch from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this script,
@@ -210,6 +211,179 @@ def cpu_baseline(sample_shape=("o", 4096, 4096), Ms=(1, 16), reps=3):
             "matmul_us": {str(m): round(mm_s[m] * 1e6, 1) for m in Ms}}
 
 
+class LibCall:
+    """Dense fp16 ``torch.matmul`` (hipBLASLt) at one call site, for the ``compare``
+    workload, on random 2:4-pruned fp16 weights of the same shape (values do not
+    matter for timing), rotating through copies like ``Call``."""
+
+    def __init__(self, name, K, N, M, kind, A, copies):
+        self.name, self.K, self.N, self.M, self.kind = name, K, N, M, kind
+        self.A = A
+        self.ws = []
+        for c in range(copies):
+            w = (torch.randn((K, N), device=A.device) * 0.02).to(torch.float16)
+            w = w * synth.prune_2_4(w)
+            self.ws.append(w)
+        self.i = 0
+
+    def __call__(self):
+        w = self.ws[self.i % len(self.ws)]
+        self.i += 1
+        return torch.matmul(self.A, w)
+
+
+class SparseLtCall:
+    """hipSPARSELt 2:4 fp16 GEMM at one call site (``libhipsparselt`` through ctypes,
+    default algorithm, fp32 compute): D[N, Mp] = W^T[N, K] (pruned and compressed by
+    the library) x X^T[K, Mp] with Mp = max(M, 16); random weights of the shape, the
+    compressed copies rotating like ``Call``."""
+
+    _lib = None
+    _handle = None
+
+    @classmethod
+    def lib(cls):
+        if cls._lib is None:
+            import ctypes
+            for name in ("libhipsparselt.so", "/opt/rocm/lib/libhipsparselt.so"):
+                try:
+                    cls._lib = ctypes.CDLL(name)
+                    break
+                except OSError:
+                    continue
+            if cls._lib is None:
+                raise RuntimeError("libhipsparselt.so not found")
+            cls._handle = ctypes.create_string_buffer(11024)
+            cls._check("hipsparseLtInit", cls._lib.hipsparseLtInit(cls._handle))
+        return cls._lib
+
+    @staticmethod
+    def _check(fn, status):
+        if status != 0:
+            raise RuntimeError(f"{fn} returned status {status}")
+
+    def __init__(self, name, K, N, M, copies, device):
+        import ctypes
+        lib = self.lib()
+        h = self._handle
+        c_i64, vp = ctypes.c_int64, ctypes.c_void_p
+        self.name, self.K, self.N, self.M = name, K, N, M
+        Mp = max(M, 16)
+        f16, row, nt, f32c, alg, strip = 2, 2, 0, 2, 0, 1
+        self.desc = [ctypes.create_string_buffer(11024) for _ in range(3)]
+        self.md, self.alg, self.plan = (ctypes.create_string_buffer(11024) for _ in range(3))
+        chk = self._check
+        chk("StructuredDescriptorInit", lib.hipsparseLtStructuredDescriptorInit(
+            h, self.desc[0], c_i64(N), c_i64(K), c_i64(K), ctypes.c_uint32(16), f16, row, 0))
+        chk("DenseDescriptorInit", lib.hipsparseLtDenseDescriptorInit(
+            h, self.desc[1], c_i64(K), c_i64(Mp), c_i64(Mp), ctypes.c_uint32(16), f16, row))
+        chk("DenseDescriptorInit", lib.hipsparseLtDenseDescriptorInit(
+            h, self.desc[2], c_i64(N), c_i64(Mp), c_i64(Mp), ctypes.c_uint32(16), f16, row))
+        chk("MatmulDescriptorInit", lib.hipsparseLtMatmulDescriptorInit(
+            h, self.md, nt, nt, self.desc[0], self.desc[1], self.desc[2], self.desc[2], f32c))
+        chk("MatmulAlgSelectionInit", lib.hipsparseLtMatmulAlgSelectionInit(h, self.alg, self.md, alg))
+        chk("MatmulPlanInit", lib.hipsparseLtMatmulPlanInit(h, self.plan, self.md, self.alg))
+        ws, csize, cbuf = ctypes.c_size_t(0), ctypes.c_size_t(0), ctypes.c_size_t(0)
+        chk("MatmulGetWorkspace", lib.hipsparseLtMatmulGetWorkspace(h, self.plan, ctypes.byref(ws)))
+        chk("SpMMACompressedSize", lib.hipsparseLtSpMMACompressedSize(h, self.plan, ctypes.byref(csize),
+                                                                      ctypes.byref(cbuf)))
+        self.B = torch.randn((K, Mp), device=device).to(torch.float16)
+        self.D = torch.empty((N, Mp), dtype=torch.float16, device=device)
+        self.ws = torch.empty(max(ws.value, 1), dtype=torch.uint8, device=device)
+        cb = torch.empty(max(cbuf.value, 1), dtype=torch.uint8, device=device)
+        stream = vp(torch.cuda.current_stream().cuda_stream)
+        self.comp = []
+        for _ in range(copies):
+            w = (torch.randn((N, K), device=device) * 0.02).to(torch.float16)
+            chk("SpMMAPrune", lib.hipsparseLtSpMMAPrune(h, self.md, vp(w.data_ptr()), vp(w.data_ptr()), strip,
+                                                         stream))
+            c = torch.empty(csize.value, dtype=torch.uint8, device=device)
+            chk("SpMMACompress", lib.hipsparseLtSpMMACompress(h, self.plan, vp(w.data_ptr()), vp(c.data_ptr()),
+                                                               vp(cb.data_ptr()), stream))
+            self.comp.append(c)
+        torch.cuda.synchronize()
+        self.alpha, self.beta = ctypes.c_float(1.0), ctypes.c_float(0.0)
+        self.i = 0
+
+    def __call__(self):
+        import ctypes
+        vp = ctypes.c_void_p
+        c = self.comp[self.i % len(self.comp)]
+        self.i += 1
+        stream = vp(torch.cuda.current_stream().cuda_stream)
+        self._check("Matmul", self.lib().hipsparseLtMatmul(
+            self._handle, self.plan, ctypes.byref(self.alpha), vp(c.data_ptr()), vp(self.B.data_ptr()),
+            ctypes.byref(self.beta), vp(self.D.data_ptr()), vp(self.D.data_ptr()), vp(self.ws.data_ptr()),
+            ctypes.byref(stream), 1))
+
+
+def time_site(fn, reps=20, samples=5):
+    """µs per call of ``fn``: a captured graph of ``reps`` calls, or (when the library
+    call cannot be captured) ``reps`` eager calls between two events; median of
+    ``samples``.  Returns (µs, method)."""
+    fn()
+    torch.cuda.synchronize()
+    try:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        run, method = g.replay, "graph"
+    except Exception:  # noqa: BLE001 - library not capturable: time it eagerly
+        torch.cuda.synchronize()
+
+        def run():
+            for _ in range(reps):
+                fn()
+        method = "eager"
+    ts = []
+    for _ in range(samples):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1000.0 / reps)
+    return statistics.median(ts), method
+
+
+def compare_libraries(device):
+    """Per call site: this library's mul_2_4 against hipBLASLt dense fp16 and
+    hipSPARSELt 2:4 fp16 (M padded to 16) at the decode (Llama-2-7B, M in {1, 16})
+    and prefill (Llama-2-70B, M in {512, 2048}) shapes."""
+    rows = []
+    cases = [(n, K, N, M) for M in (1, 16) for (n, K, N) in LLAMA7B] + \
+            [(n, K, N, M) for M in (512, 2048) for (n, K, N) in LLAMA70B]
+    for i, (name, K, N, M) in enumerate(cases):
+        decode = M <= 32
+        A = synth.make_activation(M, K, synth.SEED_BASE + M, device=device)
+        log(f"bench: compare {name} M={M}")
+        ours = Call(name, K, N, M, make_copies(K, N, synth.SEED_BASE + 1 + i, 4,
+                                               copies_for(K, N, 4) if decode else 1, device), A, marlin.mul_2_4)
+        row = {"name": name, "M": M, "K": K, "N": N}
+        row["ours_us"], _ = time_site(ours)
+        del ours
+        for kind, key in (("dense", "dense_fp16_hipblaslt_us"), ("sparse", "sparse24_fp16_hipsparselt_us")):
+            fp16_bytes = 2 * K * N // (1 if kind == "dense" else 2)
+            copies = max(2, -(-int(MALL_BYTES * 1.25) // fp16_bytes)) if decode else 1
+            try:
+                site = LibCall(name, K, N, M, kind, A, copies) if kind == "dense" else \
+                    SparseLtCall(name, K, N, M, copies, device)
+                row[key], row[key.replace("_us", "_timing")] = time_site(site)
+                del site
+            except Exception as e:  # noqa: BLE001 - report a library that does not run here
+                row[key] = None
+                row[key.replace("_us", "_error")] = f"{type(e).__name__}: {str(e)[:160]}"
+            torch.cuda.empty_cache()
+        for key in ("ours_us", "dense_fp16_hipblaslt_us", "sparse24_fp16_hipsparselt_us"):
+            if row.get(key) is not None:
+                row[key] = round(row[key], 2)
+        rows.append(row)
+    return rows
+
+
 def build_workload(args, device):
     wl = args.workload
     calls = []
@@ -294,7 +468,7 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode", "decode70b", "prefill", "w3", "meta3", "stack", "copy"])
+    p.add_argument("--workload", default="decode", choices=["decode", "decode70b", "prefill", "w3", "meta3", "stack", "copy", "compare"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -309,6 +483,19 @@ def main():
     _lib.load()
     device = "cuda:0"
     log(f"bench: workload={args.workload} steps={args.steps} warmup={args.warmup}")
+    if args.workload == "compare":
+        rows = compare_libraries(device)
+        dec = [r for r in rows if r["M"] <= 32]
+        wb = sum(synth.weight_bytes(r["K"], r["N"], 4, 128) for r in dec)
+        us = sum(r["ours_us"] for r in dec)
+        print(json.dumps({"metric": METRIC, "value": round(wb / (us * 1e3), 2), "unit": "GB/s", "n_gpus": 1,
+                          "steps": 0, "warmup": 0, "ms_per_step": round(us / 1e3, 4), "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+                          "config": {"workload": "library_comparison",
+                                     "note": "per call site, graph-replayed where capturable; value = this "
+                                             "library's decode call sites (M in {1, 16}) on weight bytes"},
+                          "compare": rows}), flush=True)
+        return
     calls, cfg = build_workload(args, device)
     log(f"bench: {len(calls)} calls per step built")
     if args.eager:
