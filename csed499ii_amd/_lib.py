@@ -28,6 +28,9 @@ SIGNATURES = {
     "marlin_hip_meta3_pack": (_i, [_vp, _vp, _ll, _vp, _i, _vp]),
     "marlin_hip_meta3_unpack": (_i, [_vp, _vp, _ll, _i, _vp]),
     "marlin_hip_expand3": (_i, [_vp, _vp, _ll, _i, _vp]),
+    "marlin_hip_native_pack": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "marlin_hip_native_unpack": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "marlin_hip_mul_2_4_native": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i]),
     "marlin_hip_last_error": (ctypes.c_char_p, []),
 }
 

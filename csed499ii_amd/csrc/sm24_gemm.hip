@@ -32,6 +32,7 @@
 
 #include "sm24_device.h"
 #include "sm24_decode.h"
+#include "sm24_native.h"
 #include "../../include/marlin_hip.h"
 
 namespace sm24 {
@@ -821,9 +822,175 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
   return MARLIN_HIP_OK;
 }
 
+// ---- lane-native layout (sm24_native.h): repack, unpack, GEMM ----
+
+int check_native_shape(int N, int K, int groupsize) {
+  if (N <= 0 || K <= 0 || N % 64 != 0 || K % 256 != 0 || !(groupsize == -1 || groupsize == 64)) {
+    set_error("marlin_hip: the native layout needs N % 64 == 0, K % 256 == 0 and groupsize 64 (dense 128) or -1");
+    return MARLIN_HIP_ERR_PROB_SHAPE;
+  }
+  return MARLIN_HIP_OK;
+}
+
+// Sets `dev` current for the scope of a call and restores the caller's device.
+struct DeviceScope {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceScope(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev && hipSetDevice(dev) != hipSuccess) {
+      set_error("marlin_hip: hipSetDevice failed");
+      ok = false;
+    }
+  }
+  ~DeviceScope() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error(std::string("marlin_hip: ") + what + " launch failed: " + hipGetErrorString(e));
+    return MARLIN_HIP_ERR_LAUNCH;
+  }
+  return MARLIN_HIP_OK;
+}
+
+int native_pack(const void* B, const void* meta, const void* s, void* W, void* X, void* S, int N, int K,
+                int groupsize, int dev, hipStream_t stream) {
+  int err = check_native_shape(N, K, groupsize);
+  if (err != MARLIN_HIP_OK) return err;
+  DeviceScope scope(dev);
+  if (!scope.ok) return MARLIN_HIP_ERR_LAUNCH;
+  const long long threads = (long long)(N / 16) * (K / 256) * 64;
+  hipLaunchKernelGGL(native_pack_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(B), static_cast<const uint16_t*>(meta),
+                     static_cast<const _Float16*>(s), static_cast<u32x4*>(W), static_cast<u32x2*>(X),
+                     static_cast<uint32_t*>(S), N, K, groupsize != -1 ? 1 : 0);
+  err = launch_status("native pack");
+  if (err == MARLIN_HIP_OK && groupsize == -1 &&
+      hipMemcpyAsync(S, s, (size_t)N * 2, hipMemcpyDeviceToDevice, stream) != hipSuccess) {
+    set_error("marlin_hip: copy of the per-column scales failed");
+    err = MARLIN_HIP_ERR_LAUNCH;
+  }
+  return err;
+}
+
+int native_unpack(const void* W, const void* X, const void* S, void* B, void* meta, void* s, int N, int K,
+                  int groupsize, int dev, hipStream_t stream) {
+  int err = check_native_shape(N, K, groupsize);
+  if (err != MARLIN_HIP_OK) return err;
+  DeviceScope scope(dev);
+  if (!scope.ok) return MARLIN_HIP_ERR_LAUNCH;
+  const long long words = (long long)(K / 32) * 2 * N;
+  hipLaunchKernelGGL(native_unpack_values_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint32_t*>(W), static_cast<uint32_t*>(B), N, K);
+  const long long metas = (long long)N * (K / 16);
+  hipLaunchKernelGGL(native_unpack_meta_kernel, dim3((unsigned)((metas + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const u32x2*>(X), static_cast<const uint32_t*>(S), static_cast<uint16_t*>(meta),
+                     static_cast<_Float16*>(s), N, K, groupsize != -1 ? 1 : 0);
+  err = launch_status("native unpack");
+  if (err == MARLIN_HIP_OK && groupsize == -1 &&
+      hipMemcpyAsync(s, S, (size_t)N * 2, hipMemcpyDeviceToDevice, stream) != hipSuccess) {
+    set_error("marlin_hip: copy of the per-column scales failed");
+    err = MARLIN_HIP_ERR_LAUNCH;
+  }
+  return err;
+}
+
+// K splits of the native kernel: the fewest that keep a split's MB activation rows
+// within 64 KiB of LDS (MARLIN_HIP_NATIVE_SPLITS raises it; read once).
+int native_splits(int MB, int K) {
+  static const int forced = env_choice("MARLIN_HIP_NATIVE_SPLITS", {1, 2, 3, 4, 5, 6, 7, 8}, 0);
+  const int nq = K / 256;
+  int s = 1;
+  while ((size_t)MB * ((nq + s - 1) / s) * 256 * 2 > 65536) s++;
+  if (forced > s) s = forced;
+  return s < nq ? s : nq;
+}
+
+template <int MB, bool G>
+void launch_native_t(const NativeArgs& a, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((sm24_native_decode_kernel<MB, 4, 4, G>), dim3((unsigned)((a.N / 16) * a.splits)),
+                     dim3(256), lds, stream, a);
+}
+
+int run_native(const void* A, const void* W, const void* X, void* C, const void* S, int N, int M, int K,
+               int groupsize, int dev, hipStream_t stream, int sms) {
+  int err = check_native_shape(N, K, groupsize);
+  if (err != MARLIN_HIP_OK) return err;
+  if (M < 0) return MARLIN_HIP_ERR_PROB_SHAPE;
+  if (M == 0) return MARLIN_HIP_OK;
+  DeviceScope scope(dev);
+  if (!scope.ok) return MARLIN_HIP_ERR_LAUNCH;
+  const bool grouped = groupsize != -1;
+  if (M > 4) {
+    // Larger batches: unpack to the reference layout in the staging buffer (on this
+    // stream) and run the reference-layout kernels on it.
+    const size_t vb = (size_t)K * N / 4, mb = (size_t)K * N / 8, sb = (size_t)(grouped ? K / 128 : 1) * N * 2;
+    void* stage = nullptr;
+    err = get_stage(dev, stream, vb + mb + sb, &stage);
+    if (err != MARLIN_HIP_OK) return err;
+    char* b = static_cast<char*>(stage);
+    err = native_unpack(W, X, S, b, b + vb, b + vb + mb, N, K, groupsize, dev, stream);
+    if (err != MARLIN_HIP_OK) return err;
+    return run(VAL4, META4, A, b, b + vb, C, b + vb + mb, N, M, K, groupsize, dev, stream, -1, -1, sms);
+  }
+  NativeArgs a{};
+  a.A = static_cast<const _Float16*>(A);
+  a.W = static_cast<const u32x4*>(W);
+  a.X = static_cast<const u32x2*>(X);
+  a.S = static_cast<const uint32_t*>(S);
+  a.s_col = static_cast<const _Float16*>(S);
+  a.C = static_cast<_Float16*>(C);
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  const int MB = M == 1 ? 1 : 4;
+  a.splits = native_splits(MB, K);
+  if (a.splits > 1) {
+    if ((size_t)(N / 16) * sizeof(uint32_t) > kCounterBytes) {
+      set_error("marlin_hip: N too large for the native kernel's split-K counters");
+      return MARLIN_HIP_ERR_PROB_SHAPE;
+    }
+    err = get_scratch(dev, stream, (size_t)(N / 16) * a.splits * MB * 16 * sizeof(float), &a.counters, &a.partial);
+    if (err != MARLIN_HIP_OK) return err;
+  }
+  const int nq = K / 256;
+  const size_t act = (size_t)MB * ((nq + a.splits - 1) / a.splits) * 256 * 2;
+  const size_t red = (size_t)4 * MB * 16 * sizeof(float);
+  const size_t lds = act > red ? act : red;
+  if (MB == 1) {
+    if (grouped) launch_native_t<1, true>(a, lds, stream);
+    else launch_native_t<1, false>(a, lds, stream);
+  } else {
+    if (grouped) launch_native_t<4, true>(a, lds, stream);
+    else launch_native_t<4, false>(a, lds, stream);
+  }
+  return launch_status("native GEMM");
+}
+
 }  // namespace sm24
 
 extern "C" {
+
+int marlin_hip_native_pack(const void* B, const void* meta, const void* s, void* Bn, void* metan, void* sn,
+                           int prob_m, int prob_k, int groupsize, int dev, hipStream_t stream) {
+  return sm24::native_pack(B, meta, s, Bn, metan, sn, prob_m, prob_k, groupsize, dev, stream);
+}
+
+int marlin_hip_native_unpack(const void* Bn, const void* metan, const void* sn, void* B, void* meta, void* s,
+                             int prob_m, int prob_k, int groupsize, int dev, hipStream_t stream) {
+  return sm24::native_unpack(Bn, metan, sn, B, meta, s, prob_m, prob_k, groupsize, dev, stream);
+}
+
+int marlin_hip_mul_2_4_native(const void* A, const void* Bn, const void* metan, void* C, const void* sn,
+                              int prob_m, int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream,
+                              int sms) {
+  return sm24::run_native(A, Bn, metan, C, sn, prob_m, prob_n, prob_k, groupsize, dev, stream, sms);
+}
 
 int marlin_hip_mul_2_4(const void* A, const void* B, const void* meta, void* C, void* s, int prob_m,
                        int prob_n, int prob_k, void* workspace, int groupsize, int dev, hipStream_t stream,

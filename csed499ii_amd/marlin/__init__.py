@@ -41,6 +41,9 @@ __all__ = [
     "pack_meta3",
     "unpack_meta3",
     "expand3",
+    "pack_native",
+    "unpack_native",
+    "mul_2_4_native",
 ]
 
 
@@ -164,6 +167,108 @@ def mul_2_4_w3(A, B3, meta, C, s, workspace, thread_k=-1, thread_m=-1, sms=-1, m
 # ---------------------------------------------------------------------------
 # Codecs
 # ---------------------------------------------------------------------------
+
+
+# ---------------------------------------------------------------------------
+# Lane-native decode layout (this library's own repack; no reference counterpart)
+# ---------------------------------------------------------------------------
+
+
+def _check_gpu(name: str, t: torch.Tensor, dtype: torch.dtype, numel: int, device):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda or t.device != device:
+        raise RuntimeError(f"{name} must be a GPU tensor on {device}")
+    if not t.is_contiguous() or t.dtype != dtype:
+        raise RuntimeError(f"{name} must be a contiguous {dtype} tensor")
+    if t.numel() != numel:
+        raise RuntimeError(f"{name} has {t.numel()} elements, expected {numel}")
+    if t.numel() and t.data_ptr() % 16:
+        raise RuntimeError(f"{name} must be 16-byte aligned")
+
+
+def pack_native(B: torch.Tensor, meta: torch.Tensor, s: torch.Tensor):
+    """Repack a ``Layer_2_4.pack`` weight (``B``, ``meta``, ``s``) into the lane-native
+    decode layout (each smfmac lane's operand words contiguous; same bytes).
+    Returns ``(Bn int32 [N/16, K/256, 64, 4], metan int16 [N/16, K/256, 64, 4], sn)``
+    with ``sn`` fp16 ``[N/16, K/256, 16, 2]`` (group size 128) or ``[1, N]``
+    (per-column scales).  Needs ``N % 64 == 0`` and ``K % 256 == 0``.  Exact inverse:
+    :func:`unpack_native`."""
+    if not (isinstance(s, torch.Tensor) and s.dim() == 2):
+        raise RuntimeError("s must be a 2-dimensional fp16 tensor")
+    N = s.shape[1]
+    if N == 0 or B.numel() * 16 % N:
+        raise RuntimeError("B does not match the scales' column count")
+    K = B.numel() * 16 // N
+    grouped = s.shape[0] != 1
+    if N % 64 or K % 256 or (grouped and s.shape[0] * 128 != K):
+        raise RuntimeError(f"the native layout needs N % 64 == 0, K % 256 == 0 and group size 128 or -1 "
+                           f"(K={K}, N={N}, {s.shape[0]} scale rows)")
+    dev = B.device
+    _check_gpu("B", B, torch.int32, K * N // 16, dev)
+    _check_gpu("meta", meta, torch.int16, K * N // 16, dev)
+    _check_gpu("s", s, torch.half, s.numel(), dev)
+    Bn = torch.empty((N // 16, K // 256, 64, 4), dtype=torch.int32, device=dev)
+    Mn = torch.empty((N // 16, K // 256, 64, 4), dtype=torch.int16, device=dev)
+    Sn = torch.empty((N // 16, K // 256, 16, 2) if grouped else (1, N), dtype=torch.half, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = _lib.load().marlin_hip_native_pack(_ptr(B), _ptr(meta), _ptr(s), _ptr(Bn), _ptr(Mn), _ptr(Sn), N, K,
+                                             64 if grouped else -1, B.get_device(), ctypes.c_void_p(stream))
+    if err != _lib.OK:
+        raise RuntimeError(_lib.last_error() or f"marlin_hip_native_pack error {err}")
+    return Bn, Mn, Sn
+
+
+def unpack_native(Bn: torch.Tensor, metan: torch.Tensor, sn: torch.Tensor):
+    """Inverse of :func:`pack_native`: returns the reference layout ``(B int32
+    [K/32, 2N], meta int16 [N, K/16], s fp16 [K/128 or 1, N])``."""
+    if not (isinstance(Bn, torch.Tensor) and Bn.dim() == 4 and tuple(Bn.shape[2:]) == (64, 4)):
+        raise RuntimeError("Bn must be the [N/16, K/256, 64, 4] tensor of pack_native")
+    N, K = 16 * Bn.shape[0], 256 * Bn.shape[1]
+    grouped = sn.numel() != N
+    dev = Bn.device
+    _check_gpu("Bn", Bn, torch.int32, K * N // 16, dev)
+    _check_gpu("metan", metan, torch.int16, K * N // 16, dev)
+    _check_gpu("sn", sn, torch.half, K * N // 128 if grouped else N, dev)
+    B = torch.empty((K // 32, 2 * N), dtype=torch.int32, device=dev)
+    meta = torch.empty((N, K // 16), dtype=torch.int16, device=dev)
+    s = torch.empty((K // 128 if grouped else 1, N), dtype=torch.half, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = _lib.load().marlin_hip_native_unpack(_ptr(Bn), _ptr(metan), _ptr(sn), _ptr(B), _ptr(meta), _ptr(s), N,
+                                               K, 64 if grouped else -1, Bn.get_device(), ctypes.c_void_p(stream))
+    if err != _lib.OK:
+        raise RuntimeError(_lib.last_error() or f"marlin_hip_native_unpack error {err}")
+    return B, meta, s
+
+
+def mul_2_4_native(A: torch.Tensor, Bn: torch.Tensor, metan: torch.Tensor, C: torch.Tensor, sn: torch.Tensor,
+                   sms: int = -1) -> None:
+    """``C = A @ W`` with ``W`` in the lane-native layout of :func:`pack_native`.  The
+    same product as :func:`mul_2_4` on the original weight (fp16 operands, fp32
+    accumulation; only the summation order differs).  Batches above 4 rows run the
+    reference-layout kernels on an unpacked copy, under :func:`mul_2_4`'s shape rules
+    (N a multiple of 128, or of 256 above 16 rows)."""
+    for name, t in (("A", A), ("C", C)):
+        if not isinstance(t, torch.Tensor) or t.dim() != 2:
+            raise RuntimeError(f"{name} must be a 2-dimensional tensor")
+    M, K = A.shape
+    N = C.shape[1]
+    if C.shape[0] != M:
+        raise RuntimeError(f"C has {C.shape[0]} rows, A has {M}")
+    if N % 64 or K % 256:
+        raise RuntimeError(f"the native layout needs N % 64 == 0 and K % 256 == 0 (K={K}, N={N})")
+    grouped = sn.numel() != N
+    dev = A.device
+    _check_gpu("A", A, torch.half, M * K, dev)
+    _check_gpu("C", C, torch.half, M * N, dev)
+    _check_gpu("Bn", Bn, torch.int32, K * N // 16, dev)
+    _check_gpu("metan", metan, torch.int16, K * N // 16, dev)
+    _check_gpu("sn", sn, torch.half, K * N // 128 if grouped else N, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    err = _lib.load().marlin_hip_mul_2_4_native(_ptr(A), _ptr(Bn), _ptr(metan), _ptr(C), _ptr(sn), N, M, K,
+                                                64 if grouped else -1, A.get_device(), ctypes.c_void_p(stream),
+                                                sms)
+    _raise_for(err, N, M, K, -1, -1, 64 if grouped else -1)
 
 
 def pack_meta3(meta: torch.Tensor) -> torch.Tensor:

@@ -91,6 +91,30 @@ int marlin_hip_meta3_unpack(const void* packed, void* out, long long n_words, in
 int marlin_hip_expand3(const void* in, void* out, long long n_groups, int dev,
                        hipStream_t stream);
 
+/* Lane-native decode layout: an offline repack of the pack() layout (B, meta, s)
+ * into per-lane operand order for the MI355X decode kernel, exactly invertible.
+ * No counterpart in the reference; it is the "offline repack to a native format"
+ * that the pack() layout's in-kernel remapping invites.  Sizes equal the reference
+ * layout's: Bn K*N/8 uint32 (K*N/4 bytes), metan K*N/16 uint16, sn K/128*N halves
+ * (groupsize 64) or N halves (groupsize -1).  Needs N % 64 == 0 and K % 256 == 0.
+ * Layout: csed499ii_amd/csrc/sm24_native.h. */
+int marlin_hip_native_pack(const void* B, const void* meta, const void* s, void* Bn, void* metan, void* sn,
+                           int prob_m, int prob_k, int groupsize, int dev, hipStream_t stream);
+
+/* Exact inverse of marlin_hip_native_pack. */
+int marlin_hip_native_unpack(const void* Bn, const void* metan, const void* sn, void* B, void* meta, void* s,
+                             int prob_m, int prob_k, int groupsize, int dev, hipStream_t stream);
+
+/* C[M,N] = A[M,K] * W[K,N] with W in the lane-native layout (same arguments as
+ * marlin_hip_mul_2_4 where they exist; automatic tiles only).  M <= 4 runs the
+ * native decode kernel (split along K, through the library's split-K scratch, when
+ * a split's activation rows exceed 64 KiB of LDS); larger M unpacks the weight into
+ * the library's staging buffer on `stream` and runs the reference-layout kernels.
+ * No counterpart in the reference (see marlin_hip_native_pack). */
+int marlin_hip_mul_2_4_native(const void* A, const void* Bn, const void* metan, void* C, const void* sn,
+                              int prob_m, int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream,
+                              int sms);
+
 /* Message describing the last MARLIN_HIP_ERR_* of the calling thread. */
 const char* marlin_hip_last_error(void);
 

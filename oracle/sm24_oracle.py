@@ -46,6 +46,10 @@ meta3_pack / meta3_unpack   encode tables CODEC:12-13 vs decode tables PAIR:11 a
 expand3                     truth table {0..7}->{4,4,9,8,E,E,D,C} (EXP3:83);
                             exhaustive over all 2^24 packed 8-code inputs
 pack_values3                round trip; bit positions 3*i (EXP3 layout)
+native_pack / native_unpack this build's own layout (no reference counterpart):
+                            exact round trip with the reference layout; the
+                            native fields read by native_dequant (stated without
+                            the reference layout) give dequant()'s weight
 ==========================  ==========================================================
 """
 from __future__ import annotations
@@ -486,3 +490,124 @@ def dequant_w3(B3, meta, s_packed, K: int, N: int, groupsize: int):
         np.put_along_axis(codes, idx[..., slot:slot + 1], vals[..., slot:slot + 1], axis=-1)
     codes = codes.reshape(N, K).T
     return dequant(None, meta, s_packed, K, N, groupsize, zero=4, codes=codes)
+
+
+# --------------------------------------------------------------------------
+# Lane-native decode layout (this build's own repack; no reference counterpart)
+# --------------------------------------------------------------------------
+
+#: Nibble of a lane word holding sparse value e (0..7) of the lane: the order in
+#: which the magic-number dequantization (masks 0x000f000f / 0x00f000f0 of the word
+#: and of the word >> 8) produces the eight fp16 operand halves.
+NATIVE_NIBBLE = np.array([0, 4, 1, 5, 2, 6, 3, 7], dtype=np.int64)
+
+
+def _native_coords(K: int, N: int):
+    """Index grids of the native layout, shape ``[N/16, K/256, 4 (h), 16 (rho), 4 (j)]``:
+    lane ``16 h + rho`` of 16-column block ``c16`` and 256-deep quad ``q`` holds, in
+    word ``j``, the 8 compressed values ``kc = 32 (4q + j) + 8h + e`` of column
+    ``n = 16 c16 + rho`` (dense K ``64 (4q+j) + 16h`` .. +16) and, in index halfword
+    ``j``, the logical metadata int16 ``meta[n, 4 (4q + j) + h]`` of those 4 groups."""
+    c16 = np.arange(N // 16)[:, None, None, None, None]
+    q = np.arange(K // 256)[None, :, None, None, None]
+    h = np.arange(4)[None, None, :, None, None]
+    rho = np.arange(16)[None, None, None, :, None]
+    j = np.arange(4)[None, None, None, None, :]
+    n = 16 * c16 + rho
+    kp = 4 * q + j
+    return n, kp, h
+
+
+def native_pack(B, meta, s_packed, K: int, N: int, groupsize: int):
+    """Reference layout -> lane-native layout.  Returns ``(Wn uint32 [N/16, K/256, 64, 4],
+    Xn uint16 [N/16, K/256, 64, 4], Sn fp16)``; ``Sn`` is ``[N/16, K/256, 16, 2]`` (the
+    scales of groups 2q, 2q+1 of column rho) for groupsize 128 and the natural-order
+    ``[1, N]`` scales for groupsize -1."""
+    if K % 256 or N % 64:
+        raise ValueError("native layout needs K % 256 == 0 and N % 64 == 0")
+    words = np.ascontiguousarray(B).view(np.uint32).reshape(K // 32, 2 * N)
+    kc, n = word_coords(K, N)
+    nib = (words[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+    sparse = np.zeros((N, K // 2), dtype=np.uint32)
+    sparse[n, kc] = nib
+    nn, kp, h = _native_coords(K, N)
+    G, Q = N // 16, K // 256
+    Wn = np.zeros((G, Q, 4, 16, 4), dtype=np.uint32)
+    for e in range(8):
+        Wn |= sparse[nn, 32 * kp + 8 * h + e] << np.uint32(4 * NATIVE_NIBBLE[e])
+    ml = meta_logical(meta, N, K)
+    Xn = np.broadcast_to(ml[nn, 4 * kp + h].astype(np.uint16), (G, Q, 4, 16, 4))
+    Wn = Wn.reshape(G, Q, 64, 4)
+    Xn = Xn.reshape(G, Q, 64, 4)
+    s_nat = unpack_scales(s_packed, K, N, groupsize)
+    if groupsize == -1:
+        Sn = s_nat.copy()
+    else:
+        g2 = np.arange(Q)[:, None, None] * 2 + np.arange(2)[None, None, :]   # [Q, 1, 2]
+        cols = (16 * np.arange(G)[:, None, None, None] + np.arange(16)[None, None, :, None])  # [G, 1, 16, 1]
+        Sn = s_nat[g2[None, :, :, :], cols]                                   # [G, Q, 16, 2]
+    return Wn, Xn, Sn
+
+
+def native_unpack(Wn, Xn, Sn, K: int, N: int, groupsize: int):
+    """Lane-native layout -> reference layout (inverse of :func:`native_pack`)."""
+    G, Q = N // 16, K // 256
+    Wn = np.asarray(Wn, dtype=np.uint32).reshape(G, Q, 4, 16, 4)
+    Xn = np.asarray(Xn, dtype=np.uint16).reshape(G, Q, 4, 16, 4)
+    nn, kp, h = _native_coords(K, N)
+    shape = np.broadcast_shapes(nn.shape, kp.shape, h.shape)
+    nn, kp, h = (np.broadcast_to(x, shape) for x in (nn, kp, h))
+    sparse = np.zeros((N, K // 2), dtype=np.uint32)
+    for e in range(8):
+        sparse[nn, 32 * kp + 8 * h + e] = (Wn >> np.uint32(4 * NATIVE_NIBBLE[e])) & 15
+    kc, n = word_coords(K, N)
+    codes = sparse[n, kc]
+    words = np.zeros(codes.shape[:2], dtype=np.uint32)
+    for p in range(8):
+        words |= codes[..., p] << np.uint32(4 * p)
+    ml = np.zeros((N, K // 16), dtype=np.uint16)
+    ml[nn, 4 * kp + h] = Xn
+    flat = np.zeros(N * (K // 16), dtype=np.uint16)
+    flat[meta_offsets(N, K // 16).ravel()] = ml.ravel()
+    _, scale_perm, scale_perm_single = get_perms_2_4()
+    if groupsize == -1:
+        s_nat = np.asarray(Sn, dtype=np.float16).reshape(1, N)
+        s_packed = s_nat.reshape(-1, 64)[:, scale_perm_single].reshape(1, N)
+    else:
+        s_nat = np.asarray(Sn, dtype=np.float16).reshape(G, Q, 16, 2).transpose(1, 3, 0, 2).reshape(K // 128, N)
+        s_packed = s_nat.reshape(-1, 64)[:, scale_perm].reshape(K // 128, N)
+    return words.view(np.int32), flat.view(np.int16).reshape(N, K // 16), s_packed
+
+
+def native_dequant(Wn, Xn, Sn, K: int, N: int, groupsize: int) -> np.ndarray:
+    """Dense fp16 ``W[K, N]`` read straight from the native layout (the meaning of
+    its fields, stated without the reference layout): lane word ``j`` nibble
+    ``NATIVE_NIBBLE[e]`` is the code of value ``e`` (group ``e // 2``, slot ``e % 2``)
+    of the lane's 4 groups, whose positions are the 2-bit fields of the lane's index
+    halfword ``j`` (nibble ``u`` = ``idx0 | idx1 << 2`` of group ``u``)."""
+    G, Q = N // 16, K // 256
+    Wn = np.asarray(Wn, dtype=np.uint32).reshape(G, Q, 4, 16, 4)
+    Xn = np.asarray(Xn, dtype=np.uint16).reshape(G, Q, 4, 16, 4).astype(np.int64)
+    W = np.zeros((N, K), dtype=np.float16)
+    if groupsize == -1:
+        s_nat = np.asarray(Sn, dtype=np.float16).reshape(1, N)
+    else:
+        s_nat = np.asarray(Sn, dtype=np.float16).reshape(G, Q, 16, 2).transpose(1, 3, 0, 2).reshape(K // 128, N)
+    gs = K if groupsize == -1 else 128
+    for c16 in range(G):
+        for q in range(Q):
+            for h in range(4):
+                for rho in range(16):
+                    n = 16 * c16 + rho
+                    for j in range(4):
+                        k0 = 64 * (4 * q + j) + 16 * h
+                        word = int(Wn[c16, q, h, rho, j])
+                        idx = int(Xn[c16, q, h, rho, j])
+                        for e in range(8):
+                            u, slot = e // 2, e % 2
+                            pos = (idx >> (4 * u + 2 * slot)) & 3
+                            code = (word >> (4 * int(NATIVE_NIBBLE[e]))) & 15
+                            k = k0 + 4 * u + pos
+                            sc = s_nat[k // gs, n]
+                            W[n, k] = np.float16(np.float16(code - 8) * sc)
+    return W.T.copy()

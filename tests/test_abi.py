@@ -62,3 +62,17 @@ def test_codec_argument_checks(built_lib):
     assert built_lib.marlin_hip_meta3_unpack(null, null, 47, 0, null) == _lib.ERR_PROB_SHAPE
     assert built_lib.marlin_hip_expand3(null, null, -1, 0, null) == _lib.ERR_PROB_SHAPE
     assert built_lib.marlin_hip_meta3_pack(null, null, 0, null, 0, null) == _lib.OK
+
+
+def test_native_host_validation(built_lib):
+    """Shapes the native layout cannot hold are refused before any launch; an empty
+    batch is a no-op."""
+    null = ctypes.c_void_p(0)
+    assert built_lib.marlin_hip_native_pack(null, null, null, null, null, null, 96, 512, 64, 0, null) == \
+        _lib.ERR_PROB_SHAPE
+    assert built_lib.marlin_hip_native_unpack(null, null, null, null, null, null, 128, 384, 64, 0, null) == \
+        _lib.ERR_PROB_SHAPE
+    assert built_lib.marlin_hip_mul_2_4_native(null, null, null, null, null, 128, 1, 512, 32, 0, null, -1) == \
+        _lib.ERR_PROB_SHAPE
+    assert built_lib.marlin_hip_mul_2_4_native(null, null, null, null, null, 128, 0, 512, 64, 0, null, -1) == \
+        _lib.OK

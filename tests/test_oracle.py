@@ -263,3 +263,51 @@ def test_values3_bit_positions_and_round_trip():
     rng = np.random.default_rng(4)
     codes = rng.integers(0, 8, size=1024)
     assert np.array_equal(o.unpack_values3(o.pack_values3(codes), 1024), codes)
+
+
+# ---------------------------------------------------------------- native layout
+
+def _packed(K, N, g, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+    mask = o.mask_2_4(w.T).T
+    gg = K if g == -1 else g
+    s = (np.abs(w * mask).reshape(K // gg, gg, N).max(1) * 2 / 15).astype(np.float16)
+    return o.pack(w, s, g, mask=mask)
+
+
+@pytest.mark.parametrize("K,N,g", [(256, 64, 128), (512, 128, -1), (768, 192, 128)])
+def test_native_round_trip_and_meaning(K, N, g):
+    """The lane-native layout is a bijection of the reference layout's bytes, and its
+    fields, read on their own terms (native_dequant), carry the same weight."""
+    B, sp, meta = _packed(K, N, g, K + N)
+    Wn, Xn, Sn = o.native_pack(B, meta, sp, K, N, g)
+    assert Wn.shape == (N // 16, K // 256, 64, 4) and Xn.shape == Wn.shape
+    B2, meta2, sp2 = o.native_unpack(Wn, Xn, Sn, K, N, g)
+    assert np.array_equal(B, B2)
+    assert np.array_equal(np.asarray(meta).view(np.uint16), np.asarray(meta2).view(np.uint16))
+    assert np.array_equal(np.asarray(sp, np.float16).view(np.uint16), np.asarray(sp2, np.float16).view(np.uint16))
+    W = o.dequant(B, meta, sp, K, N, g)
+    assert np.array_equal(W.view(np.uint16), o.native_dequant(Wn, Xn, Sn, K, N, g).view(np.uint16))
+
+
+def test_native_lane_word_positions():
+    """A single nonzero code lands in the lane word, nibble and halfword the layout
+    states: column n = 16 c16 + rho, compressed value kc = 32 (4q + j) + 8h + e at
+    nibble NATIVE_NIBBLE[e] of word j of lane 16h + rho of quad q."""
+    K, N = 512, 64
+    sparse = np.zeros((N, K // 2), dtype=np.uint32)
+    n, kc = 37, 32 * (4 * 1 + 3) + 8 * 2 + 5   # c16 2, rho 5; q 1, j 3, h 2, e 5
+    sparse[n, kc] = 9
+    kcs, ns = o.word_coords(K, N)
+    codes = sparse[ns, kcs]
+    words = np.zeros(codes.shape[:2], dtype=np.uint32)
+    for p in range(8):
+        words |= codes[..., p] << np.uint32(4 * p)
+    meta = np.zeros((N, K // 16), dtype=np.int16)
+    sp = np.ones((K // 128, N), dtype=np.float16)
+    Wn, Xn, Sn = o.native_pack(words.view(np.int32), meta, sp, K, N, 128)
+    nz = np.argwhere(Wn)
+    assert nz.tolist() == [[2, 1, 16 * 2 + 5, 3]]
+    assert Wn[2, 1, 37, 3] == 9 << (4 * int(o.NATIVE_NIBBLE[5]))
+    assert o.NATIVE_NIBBLE.tolist() == [0, 4, 1, 5, 2, 6, 3, 7]
