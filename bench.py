@@ -11,7 +11,9 @@ call streams its weight from HBM.  Prints ONE JSON line; ``value`` is the achiev
 HBM bandwidth on algorithmic compressed-weight bytes (25/64*K*N per call).
 
 Other workloads: ``decode70b`` (the decode sweep on the Llama-2-70B shapes below),
-``prefill`` (Llama-2-70B shapes, M in {512..4096}, TFLOP/s),
+``native`` / ``native70b`` (the 7B / 70B decode shapes at M in {1, 2, 4} on the
+lane-native layout of ``marlin.pack_native``), ``prefill`` (Llama-2-70B shapes, M in
+{512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
 ``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}), ``copy`` (a plain
 1 GiB device copy: the calibration run for the HBM traffic counters), ``compare``
@@ -95,9 +97,12 @@ class Call:
 def kernel_of(c) -> str:
     """The kernel the library dispatches a call to (the host rules of
     csed499ii_amd/csrc/sm24_gemm.hip: the prefill kernel, after expanding 3-bit
-    operands to 4 bits, for M >= 65 (N >= 16384), 97 (N >= 8192) or 160, with
+    operands to 4 bits, for M >= 65 (N >= 16384), 97 (N >= 4096) or 160, with
     N % 512 == 0 and K % 128 == 0; else the decode kernel up to M = 96 (launches of
-    <= 32 rows); the general kernel beyond)."""
+    <= 32 rows); the general kernel beyond; the native kernel for the lane-native
+    layout at M <= 4)."""
+    if getattr(c, "native", False):
+        return "sm24::sm24_native_decode_kernel"
     min_m = 65 if c.N >= 16384 else (97 if c.N >= 4096 else 160)
     if c.M > 32 and c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"
@@ -408,6 +413,28 @@ def build_workload(args, device):
                "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in shapes], "groupsize": 128,
                "weight_copies": copies,
                "rotated_weight_bytes": {n: copies[n] * synth.weight_bytes(K, N, bits, 128) for n, K, N in shapes}}
+    elif wl in ("native", "native70b"):
+        shapes = LLAMA70B if wl == "native70b" else LLAMA7B
+        Ms = [1, 2, 4]
+        weights, copies = {}, {}
+        for i, (name, K, N) in enumerate(shapes):
+            copies[name] = copies_for(K, N, 4)
+            base = synth.make_weight(K, N, synth.SEED_BASE + 1 + i, 128, device=device)
+            Bn, Mn, Sn = marlin.pack_native(base["B"], base["meta"], base["s"])
+            nat = {"B": Bn, "meta": Mn, "s": Sn, "bits": 4}
+            weights[name] = WeightSet([nat] + [{k: (v.clone() if isinstance(v, torch.Tensor) else v)
+                                                for k, v in nat.items()} for _ in range(copies[name] - 1)])
+
+        def native_fn(A, B, meta, C, s, ws):
+            marlin.mul_2_4_native(A, B, meta, C, s)
+        for M in Ms:
+            for name, K, N in shapes:
+                A = synth.make_activation(M, K, synth.SEED_BASE + M, device=device)
+                calls.append(Call(name, K, N, M, weights[name], A, native_fn))
+                calls[-1].native = True
+        cfg = {"workload": "native_decode_llama2_70b" if wl == "native70b" else "native_decode_llama2_7b",
+               "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in shapes], "groupsize": 128, "layout": "lane-native",
+               "weight_copies": copies}
     elif wl == "prefill":
         Ms = args.prefill_m
         for i, (name, K, N) in enumerate(LLAMA70B):
@@ -468,7 +495,8 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode", "decode70b", "prefill", "w3", "meta3", "stack", "copy", "compare"])
+    p.add_argument("--workload", default="decode", choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "stack", "copy",
+                            "compare"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
     p.add_argument("--no-cpu-baseline", action="store_true")

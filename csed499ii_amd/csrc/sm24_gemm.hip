@@ -900,21 +900,29 @@ int native_unpack(const void* W, const void* X, const void* S, void* B, void* me
   return err;
 }
 
-// K splits of the native kernel: the fewest that keep a split's MB activation rows
-// within 64 KiB of LDS (MARLIN_HIP_NATIVE_SPLITS raises it; read once).
+// Native kernel shapes, measured on MI355X (Llama-2-7B/70B shapes): one row, one
+// 16-column block per workgroup and a ring 4 quads deep, a split's activation row in
+// up to 64 KiB of LDS; 2-4 rows, two blocks per workgroup (each re-read of the
+// activation rows serves 32 columns) and a ring 2 quads deep, up to 32 KiB of rows
+// per split (more resident workgroups).  K splits: the fewest that fit; the
+// MARLIN_HIP_NATIVE_SPLITS knob raises them (read once).
+constexpr int native_ncb(int MB) { return MB == 1 ? 1 : 2; }
+
 int native_splits(int MB, int K) {
   static const int forced = env_choice("MARLIN_HIP_NATIVE_SPLITS", {1, 2, 3, 4, 5, 6, 7, 8}, 0);
   const int nq = K / 256;
+  const size_t limit = MB == 1 ? 65536 : 32768;
   int s = 1;
-  while ((size_t)MB * ((nq + s - 1) / s) * 256 * 2 > 65536) s++;
+  while ((size_t)MB * ((nq + s - 1) / s) * 256 * 2 > limit) s++;
   if (forced > s) s = forced;
   return s < nq ? s : nq;
 }
 
 template <int MB, bool G>
 void launch_native_t(const NativeArgs& a, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((sm24_native_decode_kernel<MB, 4, 4, G>), dim3((unsigned)((a.N / 16) * a.splits)),
-                     dim3(256), lds, stream, a);
+  constexpr int NCB = native_ncb(MB), D = MB == 1 ? 4 : 2;
+  hipLaunchKernelGGL((sm24_native_decode_kernel<MB, NCB, 4, D, G>),
+                     dim3((unsigned)(a.N / (16 * NCB)), (unsigned)a.splits), dim3(256), lds, stream, a);
 }
 
 int run_native(const void* A, const void* W, const void* X, void* C, const void* S, int N, int M, int K,
@@ -949,9 +957,10 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   a.N = N;
   a.K = K;
   const int MB = M == 1 ? 1 : 4;
+  const int ncb = MB == 1 ? native_ncb(1) : native_ncb(4);
   a.splits = native_splits(MB, K);
   if (a.splits > 1) {
-    if ((size_t)(N / 16) * sizeof(uint32_t) > kCounterBytes) {
+    if ((size_t)(N / (16 * ncb)) * sizeof(uint32_t) > kCounterBytes) {
       set_error("marlin_hip: N too large for the native kernel's split-K counters");
       return MARLIN_HIP_ERR_PROB_SHAPE;
     }
@@ -960,7 +969,7 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   }
   const int nq = K / 256;
   const size_t act = (size_t)MB * ((nq + a.splits - 1) / a.splits) * 256 * 2;
-  const size_t red = (size_t)4 * MB * 16 * sizeof(float);
+  const size_t red = (size_t)4 * ncb * MB * 16 * sizeof(float);
   const size_t lds = act > red ? act : red;
   if (MB == 1) {
     if (grouped) launch_native_t<1, true>(a, lds, stream);

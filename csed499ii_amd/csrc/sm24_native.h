@@ -35,8 +35,8 @@ struct NativeArgs {
   const uint32_t* S;        // lane-native scales (groupsize 128)
   const _Float16* s_col;    // per-column scales (groupsize -1), natural order
   _Float16* C;              // [M][N]
-  float* partial;           // split-K: [N/16][splits][MB][16] fp32
-  uint32_t* counters;       // split-K: [N/16] arrival counters, zero between launches
+  float* partial;           // split-K: [tiles][splits][NCB][MB][16] fp32
+  uint32_t* counters;       // split-K: [tiles] arrival counters, zero between launches
   int M, N, K, splits;
 };
 
@@ -161,70 +161,86 @@ __global__ __launch_bounds__(256) void native_unpack_meta_kernel(const u32x2* __
 
 // ---- GEMM over the lane-native layout, M <= MB (1 or 4) ----
 //
-// Workgroup: one 16-column block over the quads [q0, q1) of its K split; wave w
-// takes quads q0 + w, q0 + w + NW, ... and streams them through a ring of D
-// register slots (values, metadata and scales of one quad each), issued D quads
-// ahead, so waves never wait on each other until the end.  The MB activation rows of
-// the split are copied into LDS once (two 16-byte pieces per lane and k-pair are then
-// read back, by the lanes of real batch rows only).  Each quad is 4 smfmacs into 4
-// accumulators.  At the end the NW partial tiles are added in LDS in wave order
-// (deterministic), and with split-K handed off as in the decode kernel.
-template <int MB, int NW, int D, bool GROUPED>
+// Workgroup: NCB 16-column blocks (a tile of 16 NCB columns) over the quads
+// [q0, q1) of its K split; wave w takes quads q0 + w, q0 + w + NW, ... and streams
+// them through a ring of D register slots (values, metadata and scales of one quad
+// of every block), issued D quads ahead, so waves never wait on each other until the
+// end.  The MB activation rows of the split are copied into LDS once (two 16-byte
+// pieces per lane and k-pair are then read back, shared by the NCB blocks; wider
+// tiles cut this re-read, which every tile makes).  Each quad is 4 smfmacs per block
+// into 4 accumulators.  At the end the NW partial tiles are added in LDS in wave
+// order (deterministic), and with split-K handed off as in the decode kernel.
+template <int MB, int NCB, int NW, int D, bool GROUPED>
 __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t nlds[];
   constexpr int NT = 64 * NW;
   constexpr int APB = 8;  // activation pieces per thread per batch of loads
+  static_assert(NCB * MB * 16 <= NT, "one thread per output of the tile");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 4, rho = lane & 15;
   const int N = a.N, K = a.K, M = a.M, S = a.splits;
   const int nq = K >> 8;
-  const int ntiles = N >> 4;
-  const int z = blockIdx.x / ntiles;
-  const int c16 = blockIdx.x - z * ntiles;
-  const int q0 = (int)(((long long)nq * z) / S);
-  const int nqs = (int)(((long long)nq * (z + 1)) / S) - q0;  // >= 1 (the host keeps S <= nq)
+  const int tile = blockIdx.x, z = blockIdx.y;  // grid (N / (16 NCB), splits)
+  int q0 = 0, nqs = nq;                          // quads of this split (>= 1: the host keeps S <= nq)
+  if (S > 1) {
+    q0 = (int)((unsigned)(nq * z) / (unsigned)S);
+    nqs = (int)((unsigned)(nq * (z + 1)) / (unsigned)S) - q0;
+  }
   const int klen = nqs << 8;
   const int nr = (nqs - wave + NW - 1) / NW;  // quads of this wave (>= 0)
 
+  // Activation rows of the split into LDS (row m at byte 2*m*klen; rows >= M zero).
+  // The first batch of loads is issued before the weight ring's, so that its LDS
+  // writes wait for those loads only (loads complete in order), not for the ring.
+  const int ppr = klen >> 3;  // 16-byte pieces per row
+  const int npc = MB * ppr;
+  const u32x4* a4 = reinterpret_cast<const u32x4*>(a.A);
+  auto row_of = [&](int pc) -> int {  // pc / ppr without a division (MB <= 4)
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < MB; i++) m += pc >= i * ppr ? 1 : 0;
+    return m;
+  };
+  auto act_load = [&](int pc) -> u32x4 {
+    pc = pc < npc ? pc : npc - 1;
+    const int m = row_of(pc), pp = pc - m * ppr;
+    const int mr = m < M ? m : M - 1;
+    return a4[((size_t)mr * K + ((size_t)q0 << 8)) / 8 + pp];
+  };
+  auto act_store = [&](int pc, u32x4 v) {
+    if (pc < npc) *reinterpret_cast<u32x4*>(nlds + 16 * pc) = row_of(pc) < M ? v : (u32x4){0u, 0u, 0u, 0u};
+  };
+  u32x4 av[APB];
+#pragma unroll
+  for (int i = 0; i < APB; i++) av[i] = act_load(tid + i * NT);
+
   // ring slots: the quad of round r of this wave (clamped to the split's last)
-  u32x4 rw[D];
-  u32x2 rx[D];
-  uint32_t rs[D];
-  const size_t qbase = (size_t)c16 * nq + q0;
+  u32x4 rw[D][NCB];
+  u32x2 rx[D][NCB];
+  uint32_t rs[D][NCB];
+  const size_t qbase = (size_t)tile * NCB * nq + q0;
   auto load = [&](int d, int r) {
     int ql = wave + r * NW;
     ql = ql < nqs ? ql : nqs - 1;
-    const size_t b = qbase + ql;
-    rw[d] = a.W[b * 64 + lane];
-    rx[d] = a.X[b * 64 + lane];
-    if constexpr (GROUPED) rs[d] = a.S[b * 16 + rho];
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      const size_t b = qbase + (size_t)cb * nq + ql;
+      rw[d][cb] = a.W[b * 64 + lane];
+      rx[d][cb] = a.X[b * 64 + lane];
+      if constexpr (GROUPED) rs[d][cb] = a.S[b * 16 + rho];
+    }
   };
 #pragma unroll
   for (int d = 0; d < D; d++) load(d, d);
 
-  // activation rows of the split into LDS: row m at byte 2*m*klen (rows >= M zero)
-  const int ppr = klen >> 3;  // 16-byte pieces per row
-  const int npc = MB * ppr;
-  const u32x4* a4 = reinterpret_cast<const u32x4*>(a.A);
-  for (int base = 0; base < npc; base += APB * NT) {
-    u32x4 v[APB];
 #pragma unroll
-    for (int i = 0; i < APB; i++) {
-      int pc = base + tid + i * NT;
-      pc = pc < npc ? pc : npc - 1;
-      const int m = pc / ppr, pp = pc - m * ppr;
-      const int mr = m < M ? m : M - 1;
-      v[i] = a4[((size_t)mr * K + ((size_t)q0 << 8)) / 8 + pp];
-    }
+  for (int i = 0; i < APB; i++) act_store(tid + i * NT, av[i]);
+  for (int base = APB * NT; base < npc; base += APB * NT) {  // long splits only
 #pragma unroll
-    for (int i = 0; i < APB; i++) {
-      const int pc = base + tid + i * NT;
-      if (pc < npc) {
-        const int m = pc / ppr;
-        *reinterpret_cast<u32x4*>(nlds + 16 * pc) = m < M ? v[i] : (u32x4){0u, 0u, 0u, 0u};
-      }
-    }
+    for (int i = 0; i < APB; i++) av[i] = act_load(base + tid + i * NT);
+#pragma unroll
+    for (int i = 0; i < APB; i++) act_store(base + tid + i * NT, av[i]);
   }
   __syncthreads();
 
@@ -232,48 +248,50 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
   asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
-  float4_t acc[4];
+  float4_t acc[4][NCB];
 #pragma unroll
-  for (int j = 0; j < 4; j++) acc[j] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  half16_t act[4];  // lanes of batch rows >= MB keep zeros (their columns are never stored)
+  for (int j = 0; j < 4; j++)
 #pragma unroll
-  for (int j = 0; j < 4; j++) act[j] = (half16_t){};
+    for (int cb = 0; cb < NCB; cb++) acc[j][cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  // lanes of batch rows >= MB read row 0 (an LDS broadcast); their columns are never stored
   const uint8_t* arow = nlds + 2 * ((size_t)(rho < MB ? rho : 0) * klen + 8 * h);
 
   auto step = [&](int d, int r, bool reload) {
     const int ql = wave + r * NW;
-    if (rho < MB) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        // B operand of lane (rho, h): dense K 8h..8h+7 and 32+8h..32+8h+7 of k-pair j
-        const uint8_t* p = arow + 2 * (256 * ql + 64 * j);
-        const half8_t lo = *reinterpret_cast<const half8_t*>(p);
-        const half8_t hi = *reinterpret_cast<const half8_t*>(p + 64);
-        act[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-      }
-    }
-    const u32x4 wv = rw[d];
-    const u32x2 xv = rx[d];
+    half16_t act[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint32_t w = wv[j], w8 = w >> 8;
-      const uint32_t lo0 = (w & kMask) | kMagic, hi0 = (w & kMaskHi) | kMagic;
-      const uint32_t lo1 = (w8 & kMask) | kMagic, hi1 = (w8 & kMaskHi) | kMagic;
-      const half2_t kz = {(_Float16)1032.0f, (_Float16)1032.0f};
-      const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-      const half2_t kzh = {(_Float16)-72.0f, (_Float16)-72.0f};
-      const half2_t l0 = __builtin_bit_cast(half2_t, lo0) - kz;
-      const half2_t l1 = __builtin_bit_cast(half2_t, lo1) - kz;
-      const half2_t u0 = __builtin_bit_cast(half2_t, hi0) * k16 + kzh;
-      const half2_t u1 = __builtin_bit_cast(half2_t, hi1) * k16 + kzh;
-      half8_t aop = (half8_t){l0.x, l0.y, u0.x, u0.y, l1.x, l1.y, u1.x, u1.y};
-      if constexpr (GROUPED) {
-        const half2_t sc2 = __builtin_bit_cast(half2_t, rs[d]);
-        const _Float16 sc = sc2[j >> 1];
-        aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
+      // B operand of lane (rho, h): dense K 8h..8h+7 and 32+8h..32+8h+7 of k-pair j
+      const uint8_t* p = arow + 2 * (256 * ql + 64 * j);
+      const half8_t lo = *reinterpret_cast<const half8_t*>(p);
+      const half8_t hi = *reinterpret_cast<const half8_t*>(p + 64);
+      act[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      const u32x4 wv = rw[d][cb];
+      const u32x2 xv = rx[d][cb];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t w = wv[j], w8 = w >> 8;
+        const uint32_t lo0 = (w & kMask) | kMagic, hi0 = (w & kMaskHi) | kMagic;
+        const uint32_t lo1 = (w8 & kMask) | kMagic, hi1 = (w8 & kMaskHi) | kMagic;
+        const half2_t kz = {(_Float16)1032.0f, (_Float16)1032.0f};
+        const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const half2_t kzh = {(_Float16)-72.0f, (_Float16)-72.0f};
+        const half2_t l0 = __builtin_bit_cast(half2_t, lo0) - kz;
+        const half2_t l1 = __builtin_bit_cast(half2_t, lo1) - kz;
+        const half2_t u0 = __builtin_bit_cast(half2_t, hi0) * k16 + kzh;
+        const half2_t u1 = __builtin_bit_cast(half2_t, hi1) * k16 + kzh;
+        half8_t aop = (half8_t){l0.x, l0.y, u0.x, u0.y, l1.x, l1.y, u1.x, u1.y};
+        if constexpr (GROUPED) {
+          const half2_t sc2 = __builtin_bit_cast(half2_t, rs[d][cb]);
+          const _Float16 sc = sc2[j >> 1];
+          aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
+        }
+        if (j & 1) acc[j][cb] = smfmac64<1>(aop, act[j], acc[j][cb], xv[j >> 1]);
+        else acc[j][cb] = smfmac64<0>(aop, act[j], acc[j][cb], xv[j >> 1]);
       }
-      if (j & 1) acc[j] = smfmac64<1>(aop, act[j], acc[j], xv[j >> 1]);
-      else acc[j] = smfmac64<0>(aop, act[j], acc[j], xv[j >> 1]);
     }
     if (reload) load(d, r + D);
   };
@@ -286,52 +304,56 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
   for (int d = 0; d < D; d++)
     if (base + d < nr) step(d, base + d, false);  // uniform
 
-  // ---- reduction: lane (rho, h) holds batch row rho, columns 4h..4h+3 of the block ----
-  __syncthreads();  // every wave is done with the activation rows
+  // ---- reduction: lane (rho, h) holds batch row rho, columns 4h..4h+3 of each block ----
+  constexpr int TV = NCB * MB * 16;  // outputs of the tile: (block, row, column)
+  __syncthreads();                   // every wave is done with the activation rows
   float* red = reinterpret_cast<float*>(nlds);
   if (rho < MB) {
-    const float4_t v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    *reinterpret_cast<float4_t*>(red + (wave * MB + rho) * 16 + 4 * h) = v;
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      const float4_t v = (acc[0][cb] + acc[1][cb]) + (acc[2][cb] + acc[3][cb]);
+      *reinterpret_cast<float4_t*>(red + wave * TV + (cb * MB + rho) * 16 + 4 * h) = v;
+    }
   }
   __syncthreads();
-  const int n0 = 16 * c16;
-  const int m_out = tid >> 4, c_out = tid & 15;
+  const int cb_out = tid / (MB * 16), m_out = (tid >> 4) % MB, c_out = tid & 15;
+  const int n_out = 16 * (tile * NCB + cb_out) + c_out;
   auto write_c = [&](float v) {
     if (m_out < M) {
       _Float16 o = (_Float16)v;
-      if constexpr (!GROUPED) o = o * a.s_col[n0 + c_out];
-      a.C[(size_t)m_out * N + n0 + c_out] = o;
+      if constexpr (!GROUPED) o = o * a.s_col[n_out];
+      a.C[(size_t)m_out * N + n_out] = o;
     }
   };
-  float* const pbase = a.partial + ((size_t)c16 * S) * (MB * 16) + m_out * 16 + c_out;
-  if (tid < 16 * MB) {
-    float v = red[m_out * 16 + c_out];
+  float* const pbase = a.partial + (size_t)tile * S * TV + tid;
+  if (tid < TV) {
+    float v = red[tid];
 #pragma unroll
-    for (int w = 1; w < NW; w++) v += red[(w * MB + m_out) * 16 + c_out];
+    for (int w = 1; w < NW; w++) v += red[w * TV + tid];
     if (S == 1) write_c(v);
-    else pbase[(size_t)z * (MB * 16)] = v;
+    else pbase[(size_t)z * TV] = v;
   }
   if (S > 1) {
-    // hand-off: the stores complete before the barrier, the column block's counter is
-    // bumped after it, and the last split to arrive adds the splits' partials in
-    // split order (bit-identical whichever arrives last), writes C and resets it
+    // hand-off: the stores complete before the barrier, the tile's counter is bumped
+    // after it, and the last split to arrive adds the splits' partials in split order
+    // (bit-identical whichever arrives last), writes C and resets the counter
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __syncthreads();
     __shared__ uint32_t arrived;
     if (tid == 0)
-      arrived = __hip_atomic_fetch_add(a.counters + c16, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+      arrived = __hip_atomic_fetch_add(a.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     __syncthreads();
     if (arrived != (uint32_t)S) return;
-    if (tid == 0) __hip_atomic_store(a.counters + c16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < 16 * MB) {
+    if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < TV) {
       float v = 0.f;
       for (int z0 = 0; z0 < S; z0 += 4) {
         float t[4];
 #pragma unroll
         for (int i = 0; i < 4; i++)
-          if (z0 + i < S) t[i] = pbase[(size_t)(z0 + i) * (MB * 16)];
+          if (z0 + i < S) t[i] = pbase[(size_t)(z0 + i) * TV];
 #pragma unroll
         for (int i = 0; i < 4; i++)
           if (z0 + i < S) v = z0 + i == 0 ? t[0] : v + t[i];
