@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|decode70b|prefill|w3|meta3|stack]
 
-Default workload (BASELINE config "decode sweep"): Llama-2-7B projection shapes
+Default workload (benchmark config "decode sweep"): Llama-2-7B projection shapes
 (K x N = 4096x12288 QKV, 4096x4096 O, 4096x22016 gate/up, 11008x4096 down) at batch
 M in {1, 2, 4, 8, 16}, 2:4 INT4 weights with group-128 fp16 scales.  One step is one
 pass over the 20 (shape, M) calls, captured once in a HIP graph and replayed; the

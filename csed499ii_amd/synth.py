@@ -1,6 +1,6 @@
 """Seeded synthetic problems for the 2:4 INT4 GEMM (benchmarks and GPU tests).
 
-Inputs follow the measurement recipe of the BASELINE configs: ``A ~ N(0,1)`` fp16,
+Inputs follow the measurement recipe of the benchmark configs: ``A ~ N(0,1)`` fp16,
 ``W ~ N(0, 0.02)`` pruned to 2:4 along K (two largest ``|w|`` of each 4, ties to the
 lower index), quantized symmetric with group size 128 along K and fp16 scales (the
 quantizer of the reference's ``gen_quant4_NT``, test_2_4.py:22-37, with ``maxq`` 15

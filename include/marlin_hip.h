@@ -15,11 +15,11 @@
  * pointers): A M*K halves, B K*N/16 int32, meta K*N/16 int16, C M*N halves,
  * s (K/128 or 1)*N halves.
  *
- * Decode calls (prob_n = M <= 16) use no scratch: one workgroup owns each output
- * column tile over the whole K.  For M > 16 the planner may split K; the split-K
- * scratch (fp32 partials and arrival counters) is uncached device memory that the
- * library allocates once per device, grows on demand outside stream capture (a
- * grow during capture is refused with code 3) and never frees.  The counters are
+ * The planner may split K (decode calls at wide N or long K, large-M calls with few
+ * column tiles); the split-K scratch (fp32 partials and arrival counters) is
+ * uncached device memory that the library allocates once per device, grows on
+ * demand outside stream capture (a grow during capture is refused with code 3) and
+ * never frees.  The counters are
  * zeroed at allocation and each is returned to zero by the last workgroup that
  * arrives on it, so no buffer needs to be zeroed by the caller.  The scratch is
  * shared by all streams of a device: split-K calls that overlap in time on one
@@ -66,7 +66,7 @@ int marlin_hip_mul_2_4_meta3(const void* A, const void* B, const void* meta3, vo
  * re-packed at 3 bits per code (code of nibble p of word w at bit 3*(8w+p), the
  * kernel_experiments/3bit_encoding bit layout), codes offset by 4.  The reference
  * has no implementation of 3-bit values (its 3-bit work encodes metadata); this
- * entry point serves the BASELINE config that asks for them. */
+ * entry point serves the benchmark config that asks for them (3-bit values). */
 int marlin_hip_mul_2_4_w3(const void* A, const void* B3, const void* meta, void* C, void* s,
                           int prob_m, int prob_n, int prob_k, void* workspace, int groupsize,
                           int dev, hipStream_t stream, int thread_k, int thread_m, int sms,
@@ -95,7 +95,7 @@ int marlin_hip_expand3(const void* in, void* out, long long n_groups, int dev,
  * into per-lane operand order for the MI355X decode kernel, exactly invertible.
  * No counterpart in the reference; it is the "offline repack to a native format"
  * that the pack() layout's in-kernel remapping invites.  Sizes equal the reference
- * layout's: Bn K*N/8 uint32 (K*N/4 bytes), metan K*N/16 uint16, sn K/128*N halves
+ * layout's: Bn K*N/16 uint32 (K*N/4 bytes), metan K*N/16 uint16, sn K/128*N halves
  * (groupsize 64) or N halves (groupsize -1).  Needs N % 64 == 0 and K % 256 == 0.
  * Layout: csed499ii_amd/csrc/sm24_native.h. */
 int marlin_hip_native_pack(const void* B, const void* meta, const void* s, void* Bn, void* metan, void* sn,
@@ -108,7 +108,8 @@ int marlin_hip_native_unpack(const void* Bn, const void* metan, const void* sn, 
 /* C[M,N] = A[M,K] * W[K,N] with W in the lane-native layout (same arguments as
  * marlin_hip_mul_2_4 where they exist; automatic tiles only).  M <= 4 runs the
  * native decode kernel (split along K, through the library's split-K scratch, when
- * a split's activation rows exceed 64 KiB of LDS); larger M unpacks the weight into
+ * a split's activation rows exceed 64 KiB of LDS at M = 1 or 32 KiB at M = 2..4);
+ * larger M unpacks the weight into
  * the library's staging buffer on `stream` and runs the reference-layout kernels.
  * No counterpart in the reference (see marlin_hip_native_pack). */
 int marlin_hip_mul_2_4_native(const void* A, const void* Bn, const void* metan, void* C, const void* sn,

@@ -38,7 +38,7 @@ quantize                    closed form |q-8| <= 8, s = max|w|*2/maxq, exact
                             reconstruction of on-grid weights
 pack / unpack / dequant     round trip unpack(pack(W)) == W on tie-free inputs;
                             word_coords; scale permutation closed form
-gemm                        fp32 matmul of the dequantized weight (the BASELINE
+gemm                        fp32 matmul of the dequantized weight (the benchmark
                             oracle itself); brute-force triple loop on tiny shapes
 meta3_pack / meta3_unpack   encode tables CODEC:12-13 vs decode tables PAIR:11 are
                             mutual inverses on the 6 valid nibbles; bit-exact
@@ -344,7 +344,7 @@ def dequant(B, meta, s_packed, K: int, N: int, groupsize: int, zero: int = 8, co
 
 
 def gemm(A: np.ndarray, W: np.ndarray) -> np.ndarray:
-    """The BASELINE oracle: ``A.float() @ W.float()`` in fp32."""
+    """The benchmark oracle: ``A.float() @ W.float()`` in fp32."""
     return np.asarray(A, dtype=np.float32) @ np.asarray(W, dtype=np.float32)
 
 

@@ -1,6 +1,6 @@
 """GPU parity of the 2:4 INT4 GEMM (libmarlin_hip.so via the C ABI) against the
 CPU oracle, on the reference's own test shapes (test_2_4.py:91-135, run.py:46),
-ragged batches, the BASELINE shapes (checked through 256-column slices at full K),
+ragged batches, the benchmark shapes (checked through 256-column slices at full K),
 determinism, full overwrite of C and hipGraph replay."""
 import numpy as np
 import pytest
@@ -107,7 +107,7 @@ def test_ragged_batches(M):
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_config1_and_decode_o_proj(M):
-    """BASELINE config 1 (M=16) and the decode sweep at the O-projection shape."""
+    """Benchmark config 1 (M=16) and the decode sweep at the O-projection shape."""
     wt, A = _problem(M, 4096, 4096, 128, 20261019 + M)
     _check(wt, A, _run(wt, A), f"4096^2 M={M}")
 

@@ -1,6 +1,6 @@
 """GPU parity of the 3-bit variants: the 3-bit metadata codec and GEMM (reference
 metadata_decode experiment), the 3-bit code expansion (3bit_encoding experiment),
-and the 3-bit nonzero-value GEMM of BASELINE config 4."""
+and the 3-bit nonzero-value GEMM of benchmark config 4."""
 import numpy as np
 import pytest
 import torch
@@ -57,7 +57,7 @@ def test_meta3_gemm_equals_baseline_bit_exact(M, N, K, g):
 @pytest.mark.parametrize("M", [1, 16, 32, 256])
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 12288), (11008, 4096)])
 def test_w3_gemm_config4(M, K, N):
-    """3-bit values, Llama-2-7B shapes, M in {1, 16, 256}."""
+    """Benchmark config 4: 3-bit values, Llama-2-7B shapes, M in {1, 16, 256}."""
     wt = synth.make_weight(K, N, 4 + K + N, 128, bits=3, device=DEV)
     A = synth.make_activation(M, K, 4, device=DEV)
     C = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
