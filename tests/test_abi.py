@@ -76,3 +76,11 @@ def test_native_host_validation(built_lib):
         _lib.ERR_PROB_SHAPE
     assert built_lib.marlin_hip_mul_2_4_native(null, null, null, null, null, 128, 0, 512, 64, 0, null, -1) == \
         _lib.OK
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """There is no CPU fallback: without the built library every entry point raises."""
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libmarlin_hip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()
