@@ -87,3 +87,25 @@ def test_native_rejects_bad_shapes():
     assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), "native N=64 M=4")
     with pytest.raises(RuntimeError, match="not compatible"):
         _native_run(synth.make_activation(5, 256, 6, device=DEV), nat, 64)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (4, 11008, 4096)])
+def test_native_graph_replay_matches_eager(M, K, N):
+    """Captured native calls (one split, and K split through the scratch, grown by
+    the eager call first) replay the eager result bit for bit, with eager work and
+    synchronisations between the replays."""
+    wt = synth.make_weight(K, N, 77 + M, 128, device=DEV)
+    A = synth.make_activation(M, K, 78, device=DEV)
+    nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
+    C_eager = _native_run(A, nat, N)
+    C = torch.zeros(M, N, dtype=torch.half, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(3):
+            marlin.mul_2_4_native(A, *nat[:2], C, nat[2])
+    for _ in range(4):
+        C.fill_(float("nan"))
+        assert torch.equal(_native_run(A, nat, N), C_eager)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, C_eager)
