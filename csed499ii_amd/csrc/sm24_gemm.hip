@@ -901,26 +901,24 @@ int native_unpack(const void* W, const void* X, const void* S, void* B, void* me
 }
 
 // Native kernel shapes, measured on MI355X (Llama-2-7B/70B shapes): one row, one
-// 16-column block per workgroup and a ring 4 quads deep, a split's activation row in
-// up to 64 KiB of LDS; 2-4 rows, two blocks per workgroup (each re-read of the
-// activation rows serves 32 columns) and a ring 2 quads deep, up to 32 KiB of rows
-// per split (more resident workgroups).  K splits: the fewest that fit; the
-// MARLIN_HIP_NATIVE_SPLITS knob raises them (read once).
-constexpr int native_ncb(int MB) { return MB == 1 ? 1 : 2; }
+// 16-column block per workgroup and a ring 4 quads deep; 2-4 rows, two blocks per
+// workgroup and a ring 2 quads deep where N/32 still gives a workgroup per CU (each
+// read of the activation rows then serves 32 columns), else one block and 4 deep.
+// K split in two for 2-4 rows at K >= 16384 (down-projection of Llama-2-70B at M = 4:
+// 26.2 -> 21.1 us), else none (splits cost the 70B gate_up 3-10 %).
+// MARLIN_HIP_NATIVE_SPLITS forces the count (read once).
+int native_ncb(int MB, int N, int cus) { return MB > 1 && N / 32 >= cus ? 2 : 1; }
 
 int native_splits(int MB, int K) {
   static const int forced = env_choice("MARLIN_HIP_NATIVE_SPLITS", {1, 2, 3, 4, 5, 6, 7, 8}, 0);
   const int nq = K / 256;
-  const size_t limit = MB == 1 ? 65536 : 32768;
-  int s = 1;
-  while ((size_t)MB * ((nq + s - 1) / s) * 256 * 2 > limit) s++;
-  if (forced > s) s = forced;
+  const int s = forced > 0 ? forced : (MB > 1 && K >= 16384 ? 2 : 1);
   return s < nq ? s : nq;
 }
 
-template <int MB, bool G>
+template <int MB, int NCB, bool G>
 void launch_native_t(const NativeArgs& a, size_t lds, hipStream_t stream) {
-  constexpr int NCB = native_ncb(MB), D = MB == 1 ? 4 : 2;
+  constexpr int D = NCB == 1 ? 4 : 2;
   hipLaunchKernelGGL((sm24_native_decode_kernel<MB, NCB, 4, D, G>),
                      dim3((unsigned)(a.N / (16 * NCB)), (unsigned)a.splits), dim3(256), lds, stream, a);
 }
@@ -957,7 +955,11 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   a.N = N;
   a.K = K;
   const int MB = M == 1 ? 1 : 4;
-  const int ncb = MB == 1 ? native_ncb(1) : native_ncb(4);
+  if (sms <= 0) {
+    if (hipDeviceGetAttribute(&sms, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || sms <= 0)
+      sms = 256;
+  }
+  const int ncb = native_ncb(MB, N, sms);
   a.splits = native_splits(MB, K);
   if (a.splits > 1) {
     if ((size_t)(N / (16 * ncb)) * sizeof(uint32_t) > kCounterBytes) {
@@ -967,16 +969,18 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
     err = get_scratch(dev, stream, (size_t)(N / 16) * a.splits * MB * 16 * sizeof(float), &a.counters, &a.partial);
     if (err != MARLIN_HIP_OK) return err;
   }
-  const int nq = K / 256;
-  const size_t act = (size_t)MB * ((nq + a.splits - 1) / a.splits) * 256 * 2;
+  const size_t act = (size_t)4 * MB * 512;  // a staging slot per wave
   const size_t red = (size_t)4 * ncb * MB * 16 * sizeof(float);
   const size_t lds = act > red ? act : red;
   if (MB == 1) {
-    if (grouped) launch_native_t<1, true>(a, lds, stream);
-    else launch_native_t<1, false>(a, lds, stream);
+    if (grouped) launch_native_t<1, 1, true>(a, lds, stream);
+    else launch_native_t<1, 1, false>(a, lds, stream);
+  } else if (ncb == 1) {
+    if (grouped) launch_native_t<4, 1, true>(a, lds, stream);
+    else launch_native_t<4, 1, false>(a, lds, stream);
   } else {
-    if (grouped) launch_native_t<4, true>(a, lds, stream);
-    else launch_native_t<4, false>(a, lds, stream);
+    if (grouped) launch_native_t<4, 2, true>(a, lds, stream);
+    else launch_native_t<4, 2, false>(a, lds, stream);
   }
   return launch_status("native GEMM");
 }

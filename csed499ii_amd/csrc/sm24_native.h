@@ -164,17 +164,17 @@ __global__ __launch_bounds__(256) void native_unpack_meta_kernel(const u32x2* __
 // Workgroup: NCB 16-column blocks (a tile of 16 NCB columns) over the quads
 // [q0, q1) of its K split; wave w takes quads q0 + w, q0 + w + NW, ... and streams
 // them through a ring of D register slots (values, metadata and scales of one quad
-// of every block), issued D quads ahead, so waves never wait on each other until the
-// end.  The MB activation rows of the split are copied into LDS once (two 16-byte
-// pieces per lane and k-pair are then read back, shared by the NCB blocks; wider
-// tiles cut this re-read, which every tile makes).  Each quad is 4 smfmacs per block
+// of every block, and the quad's MB activation rows), issued D quads ahead.  When a
+// quad is due the wave writes its activation rows to its own LDS slot and reads them
+// back in B-operand order (two 16-byte pieces per lane and k-pair, shared by the NCB
+// blocks); one wave's LDS operations complete in order, so no barrier is needed and
+// waves never wait on each other until the end.  Each quad is 4 smfmacs per block
 // into 4 accumulators.  At the end the NW partial tiles are added in LDS in wave
 // order (deterministic), and with split-K handed off as in the decode kernel.
 template <int MB, int NCB, int NW, int D, bool GROUPED>
 __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t nlds[];
   constexpr int NT = 64 * NW;
-  constexpr int APB = 8;  // activation pieces per thread per batch of loads
   static_assert(NCB * MB * 16 <= NT, "one thread per output of the tile");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -187,39 +187,29 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
     q0 = (int)((unsigned)(nq * z) / (unsigned)S);
     nqs = (int)((unsigned)(nq * (z + 1)) / (unsigned)S) - q0;
   }
-  const int klen = nqs << 8;
   const int nr = (nqs - wave + NW - 1) / NW;  // quads of this wave (>= 0)
 
-  // Activation rows of the split into LDS (row m at byte 2*m*klen; rows >= M zero).
-  // The first batch of loads is issued before the weight ring's, so that its LDS
-  // writes wait for those loads only (loads complete in order), not for the ring.
-  const int ppr = klen >> 3;  // 16-byte pieces per row
-  const int npc = MB * ppr;
-  const u32x4* a4 = reinterpret_cast<const u32x4*>(a.A);
-  auto row_of = [&](int pc) -> int {  // pc / ppr without a division (MB <= 4)
-    int m = 0;
-#pragma unroll
-    for (int i = 1; i < MB; i++) m += pc >= i * ppr ? 1 : 0;
-    return m;
-  };
-  auto act_load = [&](int pc) -> u32x4 {
-    pc = pc < npc ? pc : npc - 1;
-    const int m = row_of(pc), pp = pc - m * ppr;
-    const int mr = m < M ? m : M - 1;
-    return a4[((size_t)mr * K + ((size_t)q0 << 8)) / 8 + pp];
-  };
-  auto act_store = [&](int pc, u32x4 v) {
-    if (pc < npc) *reinterpret_cast<u32x4*>(nlds + 16 * pc) = row_of(pc) < M ? v : (u32x4){0u, 0u, 0u, 0u};
-  };
-  u32x4 av[APB];
-#pragma unroll
-  for (int i = 0; i < APB; i++) av[i] = act_load(tid + i * NT);
-
-  // ring slots: the quad of round r of this wave (clamped to the split's last)
+  // Ring slots: the quad of round r of this wave (clamped to the split's last):
+  // values, metadata and scales of each block, and the quad's MB activation rows
+  // (256 halves each), which the wave stages in its own LDS slot when the quad is
+  // due (no workgroup barrier: only this wave reads it).
+  constexpr int AP = MB * 32;                  // 16-byte activation pieces per quad
+  constexpr int APL = (AP + 63) / 64;          // pieces per lane
+  constexpr int SLOTB = MB * 512;              // LDS bytes of one staged quad
   u32x4 rw[D][NCB];
   u32x2 rx[D][NCB];
   uint32_t rs[D][NCB];
+  u32x4 ra[D][APL];
   const size_t qbase = (size_t)tile * NCB * nq + q0;
+  const u32x4* a4 = reinterpret_cast<const u32x4*>(a.A);
+  // activation piece p of a quad: row p / 32 (clamped to M - 1), 16 bytes at 8 (p % 32)
+  size_t arow_off[APL];
+#pragma unroll
+  for (int i = 0; i < APL; i++) {
+    const int p = (lane + 64 * i) % AP;
+    const int m = p >> 5;
+    arow_off[i] = ((size_t)(m < M ? m : M - 1) * K + ((size_t)q0 << 8)) / 8 + (p & 31);
+  }
   auto load = [&](int d, int r) {
     int ql = wave + r * NW;
     ql = ql < nqs ? ql : nqs - 1;
@@ -230,19 +220,11 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
       rx[d][cb] = a.X[b * 64 + lane];
       if constexpr (GROUPED) rs[d][cb] = a.S[b * 16 + rho];
     }
+#pragma unroll
+    for (int i = 0; i < APL; i++) ra[d][i] = a4[arow_off[i] + (size_t)ql * 32];
   };
 #pragma unroll
   for (int d = 0; d < D; d++) load(d, d);
-
-#pragma unroll
-  for (int i = 0; i < APB; i++) act_store(tid + i * NT, av[i]);
-  for (int base = APB * NT; base < npc; base += APB * NT) {  // long splits only
-#pragma unroll
-    for (int i = 0; i < APB; i++) av[i] = act_load(base + tid + i * NT);
-#pragma unroll
-    for (int i = 0; i < APB; i++) act_store(base + tid + i * NT, av[i]);
-  }
-  __syncthreads();
 
   uint32_t kMask, kMaskHi, kMagic;
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
@@ -253,16 +235,23 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
   for (int j = 0; j < 4; j++)
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) acc[j][cb] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  // lanes of batch rows >= MB read row 0 (an LDS broadcast); their columns are never stored
-  const uint8_t* arow = nlds + 2 * ((size_t)(rho < MB ? rho : 0) * klen + 8 * h);
+  // the wave's staging slot; lanes of batch rows >= MB read row 0 (their columns are
+  // never stored); rows >= M hold row M-1 (also never stored)
+  uint8_t* const aslot = nlds + wave * SLOTB;
+  const uint8_t* const arow = aslot + 2 * ((rho < MB ? rho : 0) * 256 + 8 * h);
 
   auto step = [&](int d, int r, bool reload) {
-    const int ql = wave + r * NW;
+    // stage the quad's activation rows (each lane its pieces), then read them back in
+    // operand order; LDS operations of one wave complete in order
+#pragma unroll
+    for (int i = 0; i < APL; i++)
+      if (lane + 64 * i < AP) *reinterpret_cast<u32x4*>(aslot + 16 * (lane + 64 * i)) = ra[d][i];
+    __builtin_amdgcn_wave_barrier();
     half16_t act[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       // B operand of lane (rho, h): dense K 8h..8h+7 and 32+8h..32+8h+7 of k-pair j
-      const uint8_t* p = arow + 2 * (256 * ql + 64 * j);
+      const uint8_t* p = arow + 2 * (64 * j);
       const half8_t lo = *reinterpret_cast<const half8_t*>(p);
       const half8_t hi = *reinterpret_cast<const half8_t*>(p + 64);
       act[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
@@ -293,6 +282,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
         else acc[j][cb] = smfmac64<0>(aop, act[j], acc[j][cb], xv[j >> 1]);
       }
     }
+    __builtin_amdgcn_wave_barrier();  // the slot's reads are issued before the next quad's writes
     if (reload) load(d, r + D);
   };
   int base = 0;
