@@ -15,7 +15,8 @@ Other workloads: ``decode70b`` (the decode sweep on the Llama-2-70B shapes below
 lane-native layout of ``marlin.pack_native``), ``prefill`` (Llama-2-70B shapes, M in
 {512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
-``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}), ``copy`` (a plain
+``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}; ``stack_native`` runs
+its M = 1 pass on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``copy`` (a plain
 1 GiB device copy: the calibration run for the HBM traffic counters), ``compare``
 (per call site against hipBLASLt dense fp16 and hipSPARSELt 2:4 fp16).
 
@@ -444,18 +445,36 @@ def build_workload(args, device):
                 calls.append(Call(name, K, N, M, w, A, marlin.mul_2_4))
         cfg = {"workload": "prefill_sweep_llama2_70b", "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in LLAMA70B],
                "groupsize": 128}
-    elif wl == "stack":
+    elif wl in ("stack", "stack_native"):
         Ms = [1, 8, 32]
-        layers = []
+        native = wl == "stack_native"
+        layers, nlayers = [], []
         for l in range(32):
             layers.append({name: make_copies(K, N, synth.SEED_BASE + 1000 + 4 * l + i, 4, 1, device)
                            for i, (name, K, N) in enumerate(LLAMA7B)})
+            if native:
+                nl = {}
+                for name, ws in layers[-1].items():
+                    w = ws.copies[0]
+                    Bn, Mn, Sn = marlin.pack_native(w["B"], w["meta"], w["s"])
+                    nl[name] = WeightSet([{"B": Bn, "meta": Mn, "s": Sn, "bits": 4}])
+                nlayers.append(nl)
+
+        def native_fn(A, B, meta, C, s, ws):
+            marlin.mul_2_4_native(A, B, meta, C, s)
         for M in Ms:
             As = {K: synth.make_activation(M, K, synth.SEED_BASE + M, device=device) for _, K, _ in LLAMA7B}
             for l in range(32):
                 for name, K, N in LLAMA7B:
-                    calls.append(Call(f"L{l}.{name}", K, N, M, layers[l][name], As[K], marlin.mul_2_4))
-        cfg = {"workload": "decode_stack_32x_llama2_7b", "M": Ms, "layers": 32, "groupsize": 128}
+                    if native and M <= 4:  # what Layer_2_4.to_native() runs
+                        calls.append(Call(f"L{l}.{name}", K, N, M, nlayers[l][name], As[K], native_fn))
+                        calls[-1].native = True
+                    else:
+                        calls.append(Call(f"L{l}.{name}", K, N, M, layers[l][name], As[K], marlin.mul_2_4))
+        cfg = {"workload": "decode_stack_32x_llama2_7b" + ("_native" if native else ""), "M": Ms, "layers": 32,
+               "groupsize": 128}
+        if native:
+            cfg["layout"] = "lane-native for M <= 4 (Layer_2_4.to_native), pack() layout above"
     elif wl == "copy":
         n = (1 << 30) // 2
         src = torch.ones(n, dtype=torch.half, device=device)
@@ -495,8 +514,9 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "stack", "copy",
-                            "compare"])
+    p.add_argument("--workload", default="decode",
+                   choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "stack",
+                            "stack_native", "copy", "compare"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -578,9 +598,10 @@ def main():
            "vs_baseline": None, "dtype": "f16", "data": "synthetic", "config": cfg, "roofline": roof}
     if not args.no_per_call and args.workload != "copy":
         log("bench: per-call timing")
-        pcs = per_call_stats(calls if args.workload != "stack" else calls[:4])
+        pcs = per_call_stats(calls if not args.workload.startswith("stack") else calls[:4])
         out["per_call"] = pcs
-    if not args.no_cpu_baseline and args.workload in ("decode", "decode70b", "meta3", "w3", "stack"):
+    if not args.no_cpu_baseline and args.workload in ("decode", "decode70b", "meta3", "w3", "stack",
+                                                      "stack_native"):
         log("bench: cpu baseline (oracle)")
         out["cpu_baseline"] = cpu_baseline(("o", 8192, 8192) if args.workload == "decode70b" else ("o", 4096, 4096))
     elif not args.no_cpu_baseline:

@@ -488,11 +488,27 @@ class Layer_2_4(nn.Module):
 
     def forward(self, A):
         C = torch.empty(A.shape[:-1] + (self.s.shape[1],), dtype=A.dtype, device=A.device)
+        A2, C2 = A.view((-1, A.shape[-1])), C.view((-1, C.shape[-1]))
+        if getattr(self, "Bn", None) is not None and A2.shape[0] <= 4 and self.Bn.device == A.device:
+            mul_2_4_native(A2, self.Bn, self.metan, C2, self.sn)
+            return C
         ws = self.workspace
         if ws.device != A.device:
             ws = self.workspace = ws.to(A.device)
-        mul_2_4(A.view((-1, A.shape[-1])), self.B, self.meta, C.view((-1, C.shape[-1])), self.s, ws)
+        mul_2_4(A2, self.B, self.meta, C2, self.s, ws)
         return C
+
+    def to_native(self):
+        """Keep a lane-native copy of the packed weight (:func:`pack_native`) for
+        batches of at most 4 rows, which ``forward`` then runs on
+        :func:`mul_2_4_native`; larger batches keep using the pack() buffers, which
+        stay the module's ``state_dict``.  Needs ``infeatures % 256 == 0``; the copy
+        is as large as the packed weight.  Returns the module."""
+        Bn, metan, sn = pack_native(self.B, self.meta, self.s)
+        self.register_buffer("Bn", Bn, persistent=False)
+        self.register_buffer("metan", metan, persistent=False)
+        self.register_buffer("sn", sn, persistent=False)
+        return self
 
     def pack(self, linear, scales, trans=False, mask=None):
         """Pack a fake-quantized linear layer into the 2:4 representation.
@@ -513,6 +529,8 @@ class Layer_2_4(nn.Module):
         self.B = B.to(self.B.device)
         self.s = s.to(self.s.device)
         self.meta = meta.to(self.meta.device)
+        if getattr(self, "Bn", None) is not None:  # a native copy of the old weight is stale
+            self.to_native()
 
 
 def replace_linear(module, name_filter=lambda n: True, groupsize=-1, name=""):

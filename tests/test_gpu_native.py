@@ -109,3 +109,33 @@ def test_native_graph_replay_matches_eager(M, K, N):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(C, C_eager)
+
+
+def test_layer_to_native():
+    """Layer_2_4.to_native: batches of <= 4 rows run on the native copy, larger ones
+    on the pack() buffers; the state_dict keeps only the pack() buffers; a later
+    pack() refreshes the copy."""
+    K, N = 1024, 512
+    gen = torch.Generator().manual_seed(12)
+    w = (torch.randn((K, N), generator=gen) * 0.02).half().to(DEV)
+    q, s, ref = synth.quantize(w, 128)
+    lin = torch.nn.Linear(K, N)
+    lin.weight.data = ref
+    layer = marlin.Layer_2_4(K, N, groupsize=128).to(DEV)
+    layer.pack(lin, s, True)
+    t = {"B": layer.B.cpu().numpy(), "meta": layer.meta.cpu().numpy(), "s": layer.s.cpu().numpy(),
+         "K": K, "N": N, "groupsize": 128, "bits": 4}
+    keys = set(layer.state_dict())
+    assert layer.to_native() is layer
+    assert set(layer.state_dict()) == keys
+    for rows in (1, 3, 8):
+        x = torch.randn((rows, K), generator=gen).half().to(DEV)
+        y = layer(x)
+        torch.cuda.synchronize()
+        assert_close(y.cpu().numpy(), oracle_gemm(x.cpu().numpy(), t), f"Layer_2_4 native rows={rows}")
+    lin.weight.data = (ref * 2).half()
+    layer.pack(lin, (s * 2).half(), True)
+    t2 = {"B": layer.B.cpu().numpy(), "meta": layer.meta.cpu().numpy(), "s": layer.s.cpu().numpy(),
+          "K": K, "N": N, "groupsize": 128, "bits": 4}
+    x = torch.randn((2, K), generator=gen).half().to(DEV)
+    assert_close(layer(x).cpu().numpy(), oracle_gemm(x.cpu().numpy(), t2), "Layer_2_4 native after re-pack")
