@@ -248,3 +248,19 @@ def test_kernel_shape_errors_raise():
         _run(wt, A, thread_k=128, thread_m=128)
     with pytest.raises(RuntimeError, match=r"Problem \(m=512, n=32, k=1024\) not compatible"):
         _run(wt, A, thread_k=64, thread_m=384)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 12288), (16, 11008, 4096), (64, 4096, 22016), (512, 8192, 8192)])
+def test_per_column_scales_full_size(M, K, N):
+    """Group size -1 (one scale per output column, applied after the fp16 round of the
+    sum, marlin_cuda_kernel_nm.cu:579-585) on every kernel at full Llama sizes: the
+    decode kernel, chunked decode launches and the large-M kernel."""
+    wt, A = _problem(M, N, K, -1, 31 + M)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    assert torch.equal(_run(wt, A), C), "repeated calls differ"
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2 - 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"g=-1 {K}x{N} M={M} slice {c0}")

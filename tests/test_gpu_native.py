@@ -139,3 +139,19 @@ def test_layer_to_native():
           "K": K, "N": N, "groupsize": 128, "bits": 4}
     x = torch.randn((2, K), generator=gen).half().to(DEV)
     assert_close(layer(x).cpu().numpy(), oracle_gemm(x.cpu().numpy(), t2), "Layer_2_4 native after re-pack")
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_native_per_column_scales_full_size(M):
+    """Group size -1 on the native layout at a Llama-2-7B shape (scales applied after
+    the fp16 round of the sum, as on the pack() layout)."""
+    K, N = 4096, 12288
+    wt = synth.make_weight(K, N, 41 + M, -1, device=DEV)
+    A = synth.make_activation(M, K, 42, device=DEV)
+    nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
+    assert nat[2].shape == (1, N)
+    C = _native_run(A, nat, N)
+    t = to_cpu(wt)
+    for c0 in (0, 95, 188):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"native g=-1 M={M} slice {c0}")
