@@ -370,6 +370,16 @@ def compare_libraries(device):
                                                copies_for(K, N, 4) if decode else 1, device), A, marlin.mul_2_4)
         row = {"name": name, "M": M, "K": K, "N": N}
         row["ours_us"], _ = time_site(ours)
+        if M <= 4:  # the same weights repacked to the lane-native layout
+            nat_copies = []
+            for w in ours.wset.copies:
+                Bn, Mn, Sn = marlin.pack_native(w["B"], w["meta"], w["s"])
+                nat_copies.append({"B": Bn, "meta": Mn, "s": Sn, "bits": 4})
+
+            def native_fn(A_, B, meta, C, s, ws):
+                marlin.mul_2_4_native(A_, B, meta, C, s)
+            row["ours_native_us"], _ = time_site(Call(name, K, N, M, WeightSet(nat_copies), A, native_fn))
+            del nat_copies
         del ours
         for kind, key in (("dense", "dense_fp16_hipblaslt_us"), ("sparse", "sparse24_fp16_hipsparselt_us")):
             fp16_bytes = 2 * K * N // (1 if kind == "dense" else 2)
@@ -383,7 +393,7 @@ def compare_libraries(device):
                 row[key] = None
                 row[key.replace("_us", "_error")] = f"{type(e).__name__}: {str(e)[:160]}"
             torch.cuda.empty_cache()
-        for key in ("ours_us", "dense_fp16_hipblaslt_us", "sparse24_fp16_hipsparselt_us"):
+        for key in ("ours_us", "ours_native_us", "dense_fp16_hipblaslt_us", "sparse24_fp16_hipsparselt_us"):
             if row.get(key) is not None:
                 row[key] = round(row[key], 2)
         rows.append(row)
