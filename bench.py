@@ -11,7 +11,7 @@ call streams its weight from HBM.  Prints ONE JSON line; ``value`` is the achiev
 HBM bandwidth on algorithmic compressed-weight bytes (25/64*K*N per call).
 
 Other workloads: ``decode70b`` (the decode sweep on the Llama-2-70B shapes below),
-``native`` / ``native70b`` (the 7B / 70B decode shapes at M in {1, 2, 4} on the
+``native`` / ``native70b`` (the 7B / 70B decode shapes at M in {1, 2, 4, 8, 16} on the
 lane-native layout of ``marlin.pack_native``), ``prefill`` (Llama-2-70B shapes, M in
 {512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
@@ -101,7 +101,7 @@ def kernel_of(c) -> str:
     operands to 4 bits, for M >= 65 (N >= 16384), 97 (N >= 4096) or 160, with
     N % 512 == 0 and K % 128 == 0; else the decode kernel up to M = 96 (launches of
     <= 32 rows); the general kernel beyond; the native kernel for the lane-native
-    layout at M <= 4)."""
+    layout at M <= 16)."""
     if getattr(c, "native", False):
         return "sm24::sm24_native_decode_kernel"
     min_m = 65 if c.N >= 16384 else (97 if c.N >= 4096 else 160)
@@ -370,7 +370,7 @@ def compare_libraries(device):
                                                copies_for(K, N, 4) if decode else 1, device), A, marlin.mul_2_4)
         row = {"name": name, "M": M, "K": K, "N": N}
         row["ours_us"], _ = time_site(ours)
-        if M <= 4:  # the same weights repacked to the lane-native layout
+        if M <= 16:  # the same weights repacked to the lane-native layout
             nat_copies = []
             for w in ours.wset.copies:
                 Bn, Mn, Sn = marlin.pack_native(w["B"], w["meta"], w["s"])
@@ -426,7 +426,7 @@ def build_workload(args, device):
                "rotated_weight_bytes": {n: copies[n] * synth.weight_bytes(K, N, bits, 128) for n, K, N in shapes}}
     elif wl in ("native", "native70b"):
         shapes = LLAMA70B if wl == "native70b" else LLAMA7B
-        Ms = [1, 2, 4]
+        Ms = [1, 2, 4, 8, 16]
         weights, copies = {}, {}
         for i, (name, K, N) in enumerate(shapes):
             copies[name] = copies_for(K, N, 4)
@@ -476,7 +476,7 @@ def build_workload(args, device):
             As = {K: synth.make_activation(M, K, synth.SEED_BASE + M, device=device) for _, K, _ in LLAMA7B}
             for l in range(32):
                 for name, K, N in LLAMA7B:
-                    if native and M <= 4:  # what Layer_2_4.to_native() runs
+                    if native and M <= 16:  # what Layer_2_4.to_native() runs
                         calls.append(Call(f"L{l}.{name}", K, N, M, nlayers[l][name], As[K], native_fn))
                         calls[-1].native = True
                     else:
@@ -484,7 +484,7 @@ def build_workload(args, device):
         cfg = {"workload": "decode_stack_32x_llama2_7b" + ("_native" if native else ""), "M": Ms, "layers": 32,
                "groupsize": 128}
         if native:
-            cfg["layout"] = "lane-native for M <= 4 (Layer_2_4.to_native), pack() layout above"
+            cfg["layout"] = "lane-native for M <= 16 (Layer_2_4.to_native), pack() layout above"
     elif wl == "copy":
         n = (1 << 30) // 2
         src = torch.ones(n, dtype=torch.half, device=device)

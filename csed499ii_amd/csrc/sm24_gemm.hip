@@ -900,20 +900,41 @@ int native_unpack(const void* W, const void* X, const void* S, void* B, void* me
   return err;
 }
 
-// Native kernel shapes, measured on MI355X (Llama-2-7B/70B shapes): one row, one
-// 16-column block per workgroup and a ring 4 quads deep; 2-4 rows, two blocks per
-// workgroup and a ring 2 quads deep where N/32 still gives a workgroup per CU (each
-// read of the activation rows then serves 32 columns), else one block and 4 deep.
-// K split in two for 2-4 rows at K >= 16384 (down-projection of Llama-2-70B at M = 4:
-// 26.2 -> 21.1 us), else none (splits cost the 70B gate_up 3-10 %).
+// Native kernel shapes, measured on MI355X (Llama-2-7B/70B shapes).  One row: one
+// 16-column block per workgroup, a ring 4 quads deep, no split.  2-4 rows: two blocks
+// per workgroup and a ring 2 quads deep where N/32 still gives a workgroup per CU
+// (each read of the activation rows then serves 32 columns), else one block, 4 deep;
+// K split in two at K >= 16384 (down-projection of Llama-2-70B at M = 4: 26.2 ->
+// 21.1 us; splits cost the 70B gate_up 3-10 %).  5-16 rows (staged as 8 or 16): the
+// activation rows dominate the L2 and LDS traffic, so the widest tile (4, 2 or 1
+// blocks; ring 2 deep above one block) whose workgroups, with K split into pieces of
+// at least 10 quads, cover the CUs (split-K is a loss on shorter pieces: the 7B
+// O-projection at M = 8 went from 4.7 to 7.2 us with 4 splits of 4 quads).
 // MARLIN_HIP_NATIVE_SPLITS forces the count (read once).
-int native_ncb(int MB, int N, int cus) { return MB > 1 && N / 32 >= cus ? 2 : 1; }
+struct NativeShape {
+  int ncb, splits;
+};
 
-int native_splits(int MB, int K) {
+NativeShape native_shape(int MB, int N, int K, int cus) {
   static const int forced = env_choice("MARLIN_HIP_NATIVE_SPLITS", {1, 2, 3, 4, 5, 6, 7, 8}, 0);
   const int nq = K / 256;
-  const int s = forced > 0 ? forced : (MB > 1 && K >= 16384 ? 2 : 1);
-  return s < nq ? s : nq;
+  NativeShape sh{1, 1};
+  if (MB >= 8) {
+    // the widest tile whose workgroups fill the CUs with splits of >= 10 quads each
+    const int smax = nq / 10 < 1 ? 1 : (nq / 10 > 8 ? 8 : nq / 10);
+    for (int ncb = 4; ncb >= 1; ncb >>= 1) {
+      const int tiles = N / (16 * ncb), s = (cus + tiles - 1) / tiles;
+      if (s <= smax || ncb == 1) {
+        sh = {ncb, s < smax ? s : smax};
+        break;
+      }
+    }
+  } else if (MB > 1) {
+    sh = {N / 32 >= cus ? 2 : 1, K >= 16384 ? 2 : 1};
+  }
+  if (forced > 0) sh.splits = forced;
+  sh.splits = sh.splits < nq ? sh.splits : nq;
+  return sh;
 }
 
 template <int MB, int NCB, bool G>
@@ -932,7 +953,7 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   DeviceScope scope(dev);
   if (!scope.ok) return MARLIN_HIP_ERR_LAUNCH;
   const bool grouped = groupsize != -1;
-  if (M > 4) {
+  if (M > 16) {
     // Larger batches: unpack to the reference layout in the staging buffer (on this
     // stream) and run the reference-layout kernels on it.
     const size_t vb = (size_t)K * N / 4, mb = (size_t)K * N / 8, sb = (size_t)(grouped ? K / 128 : 1) * N * 2;
@@ -954,13 +975,14 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   a.M = M;
   a.N = N;
   a.K = K;
-  const int MB = M == 1 ? 1 : 4;
+  const int MB = M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 ? 8 : 16));
   if (sms <= 0) {
     if (hipDeviceGetAttribute(&sms, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || sms <= 0)
       sms = 256;
   }
-  const int ncb = native_ncb(MB, N, sms);
-  a.splits = native_splits(MB, K);
+  const NativeShape sh = native_shape(MB, N, K, sms);
+  const int ncb = sh.ncb;
+  a.splits = sh.splits;
   if (a.splits > 1) {
     if ((size_t)(N / (16 * ncb)) * sizeof(uint32_t) > kCounterBytes) {
       set_error("marlin_hip: N too large for the native kernel's split-K counters");
@@ -975,12 +997,30 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   if (MB == 1) {
     if (grouped) launch_native_t<1, 1, true>(a, lds, stream);
     else launch_native_t<1, 1, false>(a, lds, stream);
-  } else if (ncb == 1) {
+  } else if (MB == 4 && ncb == 1) {
     if (grouped) launch_native_t<4, 1, true>(a, lds, stream);
     else launch_native_t<4, 1, false>(a, lds, stream);
-  } else {
+  } else if (MB == 4) {
     if (grouped) launch_native_t<4, 2, true>(a, lds, stream);
     else launch_native_t<4, 2, false>(a, lds, stream);
+  } else if (MB == 8 && ncb == 1) {
+    if (grouped) launch_native_t<8, 1, true>(a, lds, stream);
+    else launch_native_t<8, 1, false>(a, lds, stream);
+  } else if (MB == 8 && ncb == 2) {
+    if (grouped) launch_native_t<8, 2, true>(a, lds, stream);
+    else launch_native_t<8, 2, false>(a, lds, stream);
+  } else if (MB == 8) {
+    if (grouped) launch_native_t<8, 4, true>(a, lds, stream);
+    else launch_native_t<8, 4, false>(a, lds, stream);
+  } else if (ncb == 1) {
+    if (grouped) launch_native_t<16, 1, true>(a, lds, stream);
+    else launch_native_t<16, 1, false>(a, lds, stream);
+  } else if (ncb == 2) {
+    if (grouped) launch_native_t<16, 2, true>(a, lds, stream);
+    else launch_native_t<16, 2, false>(a, lds, stream);
+  } else {
+    if (grouped) launch_native_t<16, 4, true>(a, lds, stream);
+    else launch_native_t<16, 4, false>(a, lds, stream);
   }
   return launch_status("native GEMM");
 }

@@ -1,4 +1,4 @@
-// Lane-native packed layout for decode, and its GEMM kernel (M <= 4).
+// Lane-native packed layout for decode, and its GEMM kernel (M <= 16).
 //
 // This layout is this library's own (an offline repack of the reference pack()
 // layout, exactly invertible); the reference has no counterpart.  Per 16-column
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void native_unpack_meta_kernel(const u32x2* __
   }
 }
 
-// ---- GEMM over the lane-native layout, M <= MB (1 or 4) ----
+// ---- GEMM over the lane-native layout, M <= MB (1, 4, 8 or 16) ----
 //
 // Workgroup: NCB 16-column blocks (a tile of 16 NCB columns) over the quads
 // [q0, q1) of its K split; wave w takes quads q0 + w, q0 + w + NW, ... and streams
@@ -175,7 +175,6 @@ template <int MB, int NCB, int NW, int D, bool GROUPED>
 __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t nlds[];
   constexpr int NT = 64 * NW;
-  static_assert(NCB * MB * 16 <= NT, "one thread per output of the tile");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 4, rho = lane & 15;
@@ -306,22 +305,29 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
     }
   }
   __syncthreads();
-  const int cb_out = tid / (MB * 16), m_out = (tid >> 4) % MB, c_out = tid & 15;
-  const int n_out = 16 * (tile * NCB + cb_out) + c_out;
-  auto write_c = [&](float v) {
+  // thread tid owns the outputs o = tid + NT i of the tile (block o / (16 MB), batch
+  // row (o / 16) % MB, column o % 16)
+  constexpr int OPT = (TV + NT - 1) / NT;
+  auto write_c = [&](int o, float v) {
+    const int m_out = (o >> 4) % MB;
+    const int n_out = 16 * (tile * NCB + o / (MB * 16)) + (o & 15);
     if (m_out < M) {
-      _Float16 o = (_Float16)v;
-      if constexpr (!GROUPED) o = o * a.s_col[n_out];
-      a.C[(size_t)m_out * N + n_out] = o;
+      _Float16 r = (_Float16)v;
+      if constexpr (!GROUPED) r = r * a.s_col[n_out];
+      a.C[(size_t)m_out * N + n_out] = r;
     }
   };
-  float* const pbase = a.partial + (size_t)tile * S * TV + tid;
-  if (tid < TV) {
-    float v = red[tid];
+  float* const pbase = a.partial + (size_t)tile * S * TV;
 #pragma unroll
-    for (int w = 1; w < NW; w++) v += red[w * TV + tid];
-    if (S == 1) write_c(v);
-    else pbase[(size_t)z * TV] = v;
+  for (int i = 0; i < OPT; i++) {
+    const int o = tid + NT * i;
+    if (o < TV) {
+      float v = red[o];
+#pragma unroll
+      for (int w = 1; w < NW; w++) v += red[w * TV + o];
+      if (S == 1) write_c(o, v);
+      else pbase[(size_t)z * TV + o] = v;
+    }
   }
   if (S > 1) {
     // hand-off: the stores complete before the barrier, the tile's counter is bumped
@@ -337,18 +343,22 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
     __syncthreads();
     if (arrived != (uint32_t)S) return;
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < TV) {
-      float v = 0.f;
-      for (int z0 = 0; z0 < S; z0 += 4) {
-        float t[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (z0 + i < S) t[i] = pbase[(size_t)(z0 + i) * TV];
+    for (int j = 0; j < OPT; j++) {
+      const int o = tid + NT * j;
+      if (o < TV) {
+        float v = 0.f;
+        for (int z0 = 0; z0 < S; z0 += 4) {
+          float t[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (z0 + i < S) v = z0 + i == 0 ? t[0] : v + t[i];
+          for (int i = 0; i < 4; i++)
+            if (z0 + i < S) t[i] = pbase[(size_t)(z0 + i) * TV + o];
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            if (z0 + i < S) v = z0 + i == 0 ? t[0] : v + t[i];
+        }
+        write_c(o, v);
       }
-      write_c(v);
     }
   }
 }

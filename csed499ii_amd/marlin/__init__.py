@@ -245,7 +245,7 @@ def mul_2_4_native(A: torch.Tensor, Bn: torch.Tensor, metan: torch.Tensor, C: to
                    sms: int = -1) -> None:
     """``C = A @ W`` with ``W`` in the lane-native layout of :func:`pack_native`.  The
     same product as :func:`mul_2_4` on the original weight (fp16 operands, fp32
-    accumulation; only the summation order differs).  Batches above 4 rows run the
+    accumulation; only the summation order differs).  Batches above 16 rows run the
     reference-layout kernels on an unpacked copy, under :func:`mul_2_4`'s shape rules
     (N a multiple of 128, or of 256 above 16 rows)."""
     for name, t in (("A", A), ("C", C)):
@@ -489,7 +489,7 @@ class Layer_2_4(nn.Module):
     def forward(self, A):
         C = torch.empty(A.shape[:-1] + (self.s.shape[1],), dtype=A.dtype, device=A.device)
         A2, C2 = A.view((-1, A.shape[-1])), C.view((-1, C.shape[-1]))
-        if getattr(self, "Bn", None) is not None and A2.shape[0] <= 4 and self.Bn.device == A.device:
+        if getattr(self, "Bn", None) is not None and A2.shape[0] <= 16 and self.Bn.device == A.device:
             mul_2_4_native(A2, self.Bn, self.metan, C2, self.sn)
             return C
         ws = self.workspace
@@ -500,7 +500,7 @@ class Layer_2_4(nn.Module):
 
     def to_native(self):
         """Keep a lane-native copy of the packed weight (:func:`pack_native`) for
-        batches of at most 4 rows, which ``forward`` then runs on
+        batches of at most 16 rows, which ``forward`` then runs on
         :func:`mul_2_4_native`; larger batches keep using the pack() buffers, which
         stay the module's ``state_dict``.  Needs ``infeatures % 256 == 0``; the copy
         is as large as the packed weight.  Returns the module."""

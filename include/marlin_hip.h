@@ -106,8 +106,8 @@ int marlin_hip_native_unpack(const void* Bn, const void* metan, const void* sn, 
                              int prob_m, int prob_k, int groupsize, int dev, hipStream_t stream);
 
 /* C[M,N] = A[M,K] * W[K,N] with W in the lane-native layout (same arguments as
- * marlin_hip_mul_2_4 where they exist; automatic tiles only).  M <= 4 runs the
- * native decode kernel (at M = 2..4 and K >= 16384 split in two along K, through
+ * marlin_hip_mul_2_4 where they exist; automatic tiles only).  M <= 16 runs the
+ * native decode kernel (at M = 2..16 and K >= 16384 split in two along K, through
  * the library's split-K scratch); larger M unpacks the weight into
  * the library's staging buffer on `stream` and runs the reference-layout kernels.
  * No counterpart in the reference (see marlin_hip_native_pack). */

@@ -37,20 +37,25 @@ def _native_run(A, nat, N):
     return C
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 13, 16, 17, 32])
 @pytest.mark.parametrize("K,N,g", [(256, 128, 128), (1024, 512, -1), (2048, 1024, 128)])
 def test_native_gemm_full_oracle(M, K, N, g):
-    """M <= 4: the native kernel (one or four batch rows); M > 4: unpack into the
-    staging buffer and the reference-layout kernels."""
+    """M <= 16: the native kernel (1, 4, 8 or 16 staged batch rows); M > 16: unpack
+    into the staging buffer and the reference-layout kernels, whose tiles need
+    N % 256 == 0 above 16 rows."""
     wt = synth.make_weight(K, N, 7 * M + K, g, device=DEV)
     A = synth.make_activation(M, K, 11 + M, device=DEV)
     nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
+    if M > 16 and N % 256:
+        with pytest.raises(RuntimeError, match="not compatible"):
+            _native_run(A, nat, N)
+        return
     C = _native_run(A, nat, N)
     assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), f"native {M}x{N}x{K} g={g}")
     assert torch.equal(_native_run(A, nat, N), C), "repeated calls differ"
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
 @pytest.mark.parametrize("K,N", [(4096, 12288), (11008, 4096), (8192, 8192), (28672, 8192)])
 def test_native_gemm_full_size_slices(K, N, M):
     """Llama-2-7B/70B decode shapes: K split when a split's activation rows would
@@ -79,17 +84,18 @@ def test_native_rejects_bad_shapes():
     wt = synth.make_weight(384, 128, 5, 128, device=DEV)  # K % 256 != 0
     with pytest.raises(RuntimeError, match="K % 256"):
         marlin.pack_native(wt["B"], wt["meta"], wt["s"])
-    # N = 64 serves M <= 4 natively; larger batches follow mul_2_4's tile rules
+    # N = 64 serves M <= 16 natively; larger batches follow mul_2_4's tile rules
     wt = synth.make_weight(256, 64, 6, 128, device=DEV)
     nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
-    A = synth.make_activation(4, 256, 6, device=DEV)
-    C = _native_run(A, nat, 64)
-    assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), "native N=64 M=4")
+    for m in (4, 16):
+        A = synth.make_activation(m, 256, 6, device=DEV)
+        C = _native_run(A, nat, 64)
+        assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), f"native N=64 M={m}")
     with pytest.raises(RuntimeError, match="not compatible"):
-        _native_run(synth.make_activation(5, 256, 6, device=DEV), nat, 64)
+        _native_run(synth.make_activation(17, 256, 6, device=DEV), nat, 64)
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (4, 11008, 4096)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (4, 11008, 4096), (16, 4096, 4096)])
 def test_native_graph_replay_matches_eager(M, K, N):
     """Captured native calls (one split, and K split through the scratch, grown by
     the eager call first) replay the eager result bit for bit, with eager work and
@@ -112,7 +118,7 @@ def test_native_graph_replay_matches_eager(M, K, N):
 
 
 def test_layer_to_native():
-    """Layer_2_4.to_native: batches of <= 4 rows run on the native copy, larger ones
+    """Layer_2_4.to_native: batches of <= 16 rows run on the native copy, larger ones
     on the pack() buffers; the state_dict keeps only the pack() buffers; a later
     pack() refreshes the copy."""
     K, N = 1024, 512
@@ -128,7 +134,7 @@ def test_layer_to_native():
     keys = set(layer.state_dict())
     assert layer.to_native() is layer
     assert set(layer.state_dict()) == keys
-    for rows in (1, 3, 8):
+    for rows in (1, 3, 8, 16, 40):
         x = torch.randn((rows, K), generator=gen).half().to(DEV)
         y = layer(x)
         torch.cuda.synchronize()
@@ -141,7 +147,7 @@ def test_layer_to_native():
     assert_close(layer(x).cpu().numpy(), oracle_gemm(x.cpu().numpy(), t2), "Layer_2_4 native after re-pack")
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
 def test_native_per_column_scales_full_size(M):
     """Group size -1 on the native layout at a Llama-2-7B shape (scales applied after
     the fp16 round of the sum, as on the pack() layout)."""
