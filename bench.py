@@ -16,7 +16,7 @@ lane-native layout of ``marlin.pack_native``), ``prefill`` (Llama-2-70B shapes, 
 {512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
 ``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}; ``stack_native`` runs
-its M = 1 pass on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``copy`` (a plain
+its M = 1 and M = 8 passes on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``copy`` (a plain
 1 GiB device copy: the calibration run for the HBM traffic counters), ``compare``
 (per call site against hipBLASLt dense fp16 and hipSPARSELt 2:4 fp16).
 
