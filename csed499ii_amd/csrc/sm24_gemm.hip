@@ -908,23 +908,30 @@ int native_unpack(const void* W, const void* X, const void* S, void* B, void* me
 // 21.1 us; splits cost the 70B gate_up 3-10 %).  5-16 rows (staged as 8 or 16): the
 // activation rows dominate the L2 and LDS traffic, so the widest tile (4, 2 or 1
 // blocks; ring 2 deep above one block) whose workgroups, with K split into pieces of
-// at least 10 quads, cover the CUs (split-K is a loss on shorter pieces: the 7B
-// O-projection at M = 8 went from 4.7 to 7.2 us with 4 splits of 4 quads).
-// MARLIN_HIP_NATIVE_SPLITS forces the count (read once).
+// at least 10 quads, cover 60 % of the CUs, split only when the tiles alone do not
+// (a sweep of blocks x splits on the Llama-2 shapes: four blocks unsplit on 160-192
+// workgroups beat two blocks or a split, 70B QKV at M = 16 14.0 against 16.8 us;
+// split-K is a loss on short pieces: 7B O at M = 8 4.7 us unsplit, 8.1 us in 4).
+// MARLIN_HIP_NATIVE_SPLITS forces the count and, at 5-16 rows, MARLIN_HIP_NATIVE_BLOCKS
+// the blocks per workgroup (each read once).
 struct NativeShape {
   int ncb, splits;
 };
 
 NativeShape native_shape(int MB, int N, int K, int cus) {
   static const int forced = env_choice("MARLIN_HIP_NATIVE_SPLITS", {1, 2, 3, 4, 5, 6, 7, 8}, 0);
+  static const int forced_ncb = env_choice("MARLIN_HIP_NATIVE_BLOCKS", {1, 2, 4}, 0);
   const int nq = K / 256;
   NativeShape sh{1, 1};
   if (MB >= 8) {
-    // the widest tile whose workgroups fill the CUs with splits of >= 10 quads each
+    // the widest tile whose workgroups, with splits of >= 10 quads each, cover 60 %
+    // of the CUs; split only below that (then up to one workgroup per CU)
     const int smax = nq / 10 < 1 ? 1 : (nq / 10 > 8 ? 8 : nq / 10);
+    const int fill = (3 * cus + 4) / 5;
     for (int ncb = 4; ncb >= 1; ncb >>= 1) {
-      const int tiles = N / (16 * ncb), s = (cus + tiles - 1) / tiles;
-      if (s <= smax || ncb == 1) {
+      const int tiles = N / (16 * ncb);
+      if (tiles * smax >= fill || ncb == 1) {
+        const int s = tiles >= fill ? 1 : (cus + tiles - 1) / tiles;
         sh = {ncb, s < smax ? s : smax};
         break;
       }
@@ -932,6 +939,7 @@ NativeShape native_shape(int MB, int N, int K, int cus) {
   } else if (MB > 1) {
     sh = {N / 32 >= cus ? 2 : 1, K >= 16384 ? 2 : 1};
   }
+  if (MB >= 8 && forced_ncb > 0) sh.ncb = forced_ncb;
   if (forced > 0) sh.splits = forced;
   sh.splits = sh.splits < nq ? sh.splits : nq;
   return sh;
