@@ -17,6 +17,7 @@ import sys
 PKG = pathlib.Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libmarlin_hip.so"
+PROBE_LIB = PKG / "libmarlin_probe.so"
 ARCH = "gfx950"
 
 
@@ -67,24 +68,31 @@ def _finish(proc: subprocess.Popen, what: str, verbose: bool) -> None:
 
 def build(verbose: bool = False) -> pathlib.Path:
     """Compile every source to an object (in parallel), then link
-    ``csed499ii_amd/libmarlin_hip.so`` (always rebuilds)."""
+    ``csed499ii_amd/libmarlin_hip.so`` (the GEMM library, from ``csrc/*.hip``) and
+    ``csed499ii_amd/libmarlin_probe.so`` (bench.py's measurement aids, from
+    ``csrc/probe/*.hip``); always rebuilds both."""
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    probe_srcs = sorted((CSRC / "probe").glob("*.hip"))
     obj_dir = PKG / "_build"
     obj_dir.mkdir(exist_ok=True)
-    objs, procs = [], []
-    for src in srcs:
+    objs, probe_objs, procs = [], [], []
+    for src in srcs + probe_srcs:
         obj = obj_dir / (src.stem + ".o")
-        objs.append(obj)
+        (probe_objs if src in probe_srcs else objs).append(obj)
         cmd = [hipcc(), *compile_flags(), *EXTRA_FLAGS.get(src.name, []), "-c", "-o", str(obj), str(src)]
         procs.append((_run(cmd, verbose), src.name))
     for proc, name in procs:
         _finish(proc, name, verbose)
-    tmp = LIB.with_suffix(".so.tmp")
-    link = _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", str(tmp), *map(str, objs)], verbose)
-    _finish(link, "link", verbose)
-    os.replace(tmp, LIB)
+    for lib, lib_objs in ((LIB, objs), (PROBE_LIB, probe_objs)):
+        if not lib_objs:
+            continue
+        tmp = lib.with_suffix(".so.tmp")
+        link = _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-o", str(tmp), *map(str, lib_objs)],
+                    verbose)
+        _finish(link, f"link of {lib.name}", verbose)
+        os.replace(tmp, lib)
     return LIB
 
 

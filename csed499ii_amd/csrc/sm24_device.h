@@ -118,6 +118,7 @@ struct GemmArgs {
 constexpr int kDecodeMaxM = 32;       // largest batch of one decode launch (two 16-row blocks)
 constexpr int kDecodeChunkMaxM = 96;  // largest batch run as several decode launches
 constexpr int kPreTileCols = 512;
+constexpr int kPreThreads = 512;  // one wave per 64-column chunk of the tile
 constexpr size_t kPreSplitBytes = 512 * 128 * sizeof(float);  // fp32 partial of one tile
 hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream);
 

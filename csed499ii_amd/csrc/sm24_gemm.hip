@@ -303,23 +303,55 @@ struct Scratch {
   size_t bytes = 0;
 };
 
-// Split-K scratch (arrival counters + fp32 partials), one per device and shared by
-// every stream: calls that overlap in time on one device must not both split K.
-// Buffers are never freed: a captured graph may still refer to an old one.
+// Split-K scratch (arrival counters + fp32 partials) and operand staging buffers,
+// one per (device, stream): calls on different streams never share one, so they may
+// overlap in time (the reference gets the same safety from one workspace per layer).
+// Calls on one stream are ordered, so they may share theirs.  Buffers are never
+// freed: a captured graph may still refer to an old one.
+using StreamKey = std::pair<int, hipStream_t>;
 std::mutex g_scratch_mu;
-std::map<int, Scratch> g_scratch;
+std::map<StreamKey, Scratch> g_scratch;
 std::map<int, void*> g_zeros;
 
-constexpr size_t kZeroBytes = 256;
+bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
 
-// A small zero-filled buffer per device (read by lanes that have no activation row).
-int get_zeros(int dev, const _Float16** out) {
+// The library's static device scratch: the zero block that the decode and general
+// kernels read in place of activation rows that do not exist (rows past M, k-blocks
+// past K).  Every device holds its own copy from module load until the process ends;
+// no kernel writes it, so calls on any stream may share it.  It is all the scratch
+// that a call planned without K splits needs.
+constexpr size_t kScratchBytes = 256;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+__global__ void fill_zero_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Device address of `scratch` on `dev` (the caller has made `dev` current).  Looked up
+// once per device with hipGetSymbolAddress; the array's name itself is only a host
+// stand-in.  The first lookup also clears the block with a fill kernel on `stream`
+// (it is zero from module load; the fill is a guard that costs one launch per device
+// and process).
+int get_zeros(int dev, hipStream_t stream, const _Float16** out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   void*& z = g_zeros[dev];
   if (!z) {
     void* p = nullptr;
-    if (hipMalloc(&p, kZeroBytes) != hipSuccess || hipMemset(p, 0, kZeroBytes) != hipSuccess) {
-      set_error("marlin_hip: allocation of the zero buffer failed");
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error(std::string("marlin_hip: hipGetSymbolAddress of the static scratch failed: ") +
+                hipGetErrorString(e));
+      return MARLIN_HIP_ERR_LAUNCH;
+    }
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(64), 0, stream, static_cast<uint32_t*>(p),
+                       (int)(kScratchBytes / 4));
+    const hipError_t le = hipGetLastError();
+    if (le != hipSuccess) {
+      set_error(std::string("marlin_hip: clearing the static scratch failed: ") + hipGetErrorString(le));
       return MARLIN_HIP_ERR_LAUNCH;
     }
     z = p;
@@ -330,16 +362,21 @@ int get_zeros(int dev, const _Float16** out) {
 
 constexpr size_t kCounterBytes = 64 * 1024;  // up to 16384 (chunk, batch-tile) counters
 
+// The split-K scratch of (dev, stream), grown to hold `partial_bytes` of partials.
+// A buffer cannot be allocated while the stream is being captured into a graph: then,
+// if the stream's scratch is too small, *counters and *partial come back null and
+// the caller runs the call without splitting K (same result, one workgroup per tile;
+// an eager call of the same shape on the capturing stream before the capture
+// avoids that).
 int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** counters, float** partial) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  Scratch& s = g_scratch[dev];
+  Scratch& s = g_scratch[StreamKey(dev, stream)];
   const size_t need = kCounterBytes + partial_bytes;
   if (s.bytes < need) {
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone) {
-      set_error("marlin_hip: the split-K scratch would have to grow during stream capture; make one "
-                "call of the same (or a larger) shape on this device before capturing");
-      return MARLIN_HIP_ERR_LAUNCH;
+    if (capturing(stream)) {
+      *counters = nullptr;
+      *partial = nullptr;
+      return MARLIN_HIP_OK;
     }
     size_t nb = need > 2 * s.bytes ? need : 2 * s.bytes;
     void* p = nullptr;
@@ -365,19 +402,19 @@ int get_scratch(int dev, hipStream_t stream, size_t partial_bytes, uint32_t** co
 }
 
 // Staging buffer for operands expanded to the large-M kernel's 4-bit formats (3-bit
-// values, 3-bit metadata), one per device and shared by every stream: calls that
-// overlap in time on one device must not both expand.  Ordinary device memory
-// (written and read by kernels of the same stream); grows, never freed.
-std::map<int, Scratch> g_stage;
+// values, 3-bit metadata, the lane-native layout above 16 rows), one per (device,
+// stream).  Ordinary device memory (written and read by kernels of the same stream);
+// grows, never freed.
+std::map<StreamKey, Scratch> g_stage;
 
 int get_stage(int dev, hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  Scratch& s = g_stage[dev];
+  Scratch& s = g_stage[StreamKey(dev, stream)];
   if (s.bytes < bytes) {
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone) {
-      set_error("marlin_hip: the operand staging buffer would have to grow during stream capture; make one "
-                "call of the same (or a larger) shape on this device before capturing");
+    if (capturing(stream)) {
+      set_error("marlin_hip: the operand staging buffer of this stream would have to grow during stream "
+                "capture; make one call of the same (or a larger) shape on the capturing stream before "
+                "capturing");
       return MARLIN_HIP_ERR_LAUNCH;
     }
     const size_t nb = bytes > 2 * s.bytes ? bytes : 2 * s.bytes;
@@ -522,11 +559,11 @@ struct DecodeShape {
   int tc, nw, splits;
   bool deep;  // register ring: deep (more stages in flight) or 16 VGPRs
 };
+bool decode_deep(int K, int splits);
 DecodeShape decode_shape(int M, int N, int K, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   static const int forced_splits = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
-  static const int forced_deep = env_choice("MARLIN_HIP_DECODE_DEEP", {0, 1}, -1);
   DecodeShape d;
   const bool wide32 = N / 32 >= 2 * cus;
   const bool narrow = 2 * (N / 64) < cus;
@@ -562,11 +599,22 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   const int nst = (K / 32 + d.nw * kpw - 1) / (d.nw * kpw);
   if (d.splits > nst) d.splits = nst;
   if ((size_t)(N / d.tc) * sizeof(uint32_t) > kCounterBytes) d.splits = 1;
-  // Register ring depth: deep for long K per split (one workgroup per CU streams more
-  // stages at once), shallow for K <= 8192 (more resident workgroups); measured on
-  // the Llama-2-7B shapes (K = 4096 and 11008).
-  d.deep = forced_deep >= 0 ? forced_deep == 1 : K / d.splits > 8192;
+  d.deep = decode_deep(K, d.splits);
   return d;
+}
+
+// Register ring depth: deep for long K per split (one workgroup per CU streams more
+// stages at once), shallow for K <= 8192 (more resident workgroups); measured on
+// the Llama-2-7B shapes (K = 4096 and 11008).  MARLIN_HIP_DECODE_DEEP overrides.
+bool decode_deep(int K, int splits) {
+  static const int forced_deep = env_choice("MARLIN_HIP_DECODE_DEEP", {0, 1}, -1);
+  return forced_deep >= 0 ? forced_deep == 1 : K / splits > 8192;
+}
+
+// The same decode shape without a K split (no split-K scratch available or wanted).
+void decode_unsplit(DecodeShape& d, int K) {
+  d.splits = 1;
+  d.deep = decode_deep(K, 1);
 }
 
 // Padded batch of the decode kernel: 1, 4 (activations staged through LDS), 16 or 32
@@ -662,176 +710,6 @@ int validate(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, in
   return MARLIN_HIP_OK;
 }
 
-int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C, void* s, int prob_m,
-        int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream, int thread_k, int thread_m,
-        int sms) {
-  int err = validate(prob_m, prob_n, prob_k, groupsize, thread_k, thread_m);
-  if (err != MARLIN_HIP_OK) return err;
-  if (prob_m == 0 || prob_n == 0 || prob_k == 0) return MARLIN_HIP_OK;
-  // The 64-column chunk and 32-deep k-block of the packed layouts (and 128-deep
-  // scale groups) are this implementation's own granularity.
-  if (prob_m % 64 != 0 || prob_k % 32 != 0 || (groupsize != -1 && prob_k % 128 != 0)) {
-    set_error("marlin_hip: N must be a multiple of 64 and K of 32 (128 when grouped)");
-    return MARLIN_HIP_ERR_PROB_SHAPE;
-  }
-  int prev = -1;
-  if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-  if (prev != dev && hipSetDevice(dev) != hipSuccess) {
-    set_error("marlin_hip: hipSetDevice failed");
-    return MARLIN_HIP_ERR_LAUNCH;
-  }
-  if (sms <= 0) {
-    if (hipDeviceGetAttribute(&sms, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || sms <= 0)
-      sms = 256;
-  }
-  const int M = prob_n, N = prob_m, K = prob_k;
-  // Decode kernel: M <= 32, or, below the large-M kernel's threshold, up to 96 rows as
-  // consecutive launches of <= 32 rows (measured on the Llama-2-7B shapes: o at M = 64
-  // 17.8 against 28.8 us, down at M = 96 40.5 against 49.7 us for the general kernel).
-  const bool chunked = M > kDecodeMaxM && M <= kDecodeChunkMaxM && !prefill_fits(M, N, K, VAL4, META4);
-  if (M <= kDecodeMaxM || chunked) {
-    err = MARLIN_HIP_OK;
-    for (int r0 = 0; r0 < M && err == MARLIN_HIP_OK; r0 += kDecodeMaxM) {
-      const int mc = M - r0 < kDecodeMaxM ? M - r0 : kDecodeMaxM;
-      GemmArgs d{};
-      d.A = static_cast<const _Float16*>(A) + (size_t)r0 * K;
-      d.B = B;
-      d.meta = meta;
-      d.s = static_cast<const _Float16*>(s);
-      d.C = static_cast<_Float16*>(C) + (size_t)r0 * N;
-      d.M = mc;
-      d.N = N;
-      d.K = K;
-      const DecodeShape shape = decode_shape(mc, N, K, sms);
-      d.splits = shape.splits;
-      err = get_zeros(dev, &d.zeros);
-      if (err == MARLIN_HIP_OK && d.splits > 1) {
-        const int rows = decode_batch(mc) > 16 ? decode_batch(mc) : 16;
-        err = get_scratch(dev, stream, (size_t)(N / shape.tc) * d.splits * rows * shape.tc * sizeof(float),
-                          &d.counters, &d.partial);
-      }
-      if (err == MARLIN_HIP_OK) {
-        const hipError_t e = launch_decode(d, shape, vf, mf, groupsize != -1, stream);
-        if (e != hipSuccess) {
-          set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
-          err = MARLIN_HIP_ERR_LAUNCH;
-        }
-      }
-    }
-    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-    return err;
-  }
-  if (prefill_fits(M, N, K, VAL4, META4) && (vf != VAL4 || mf != META4)) {
-    // 3-bit values or metadata at large M: expand them into the 4-bit layouts on this
-    // stream, then the large-M kernel reads the expanded copy.
-    const size_t vbytes = vf == VAL3 ? (size_t)K * N / 4 : 0, mbytes = mf == META3 ? (size_t)K * N / 8 : 0;
-    void* stage = nullptr;
-    err = get_stage(dev, stream, vbytes + mbytes, &stage);
-    if (err != MARLIN_HIP_OK) {
-      if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-      return err;
-    }
-    if (vf == VAL3) {
-      const long long quads = (long long)K * N / 64;
-      hipLaunchKernelGGL(w3_to_w4_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                         static_cast<const uint32_t*>(B), static_cast<u32x4*>(stage), quads);
-      B = stage;
-    }
-    if (mf == META3) {
-      void* m4 = static_cast<char*>(stage) + vbytes;
-      err = marlin_hip_meta3_unpack(meta, m4, (long long)K * N / 8 / 4 * 3 / 4, dev, stream);
-      if (err != MARLIN_HIP_OK) {
-        if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-        return err;
-      }
-      meta = m4;
-    }
-    vf = VAL4;
-    mf = META4;
-  }
-  if (prefill_fits(M, N, K, vf, mf)) {
-    GemmArgs p{};
-    p.A = static_cast<const _Float16*>(A);
-    p.B = B;
-    p.meta = meta;
-    p.s = static_cast<const _Float16*>(s);
-    p.C = static_cast<_Float16*>(C);
-    p.M = M;
-    p.N = N;
-    p.K = K;
-    const int tiles = (N / kPreTileCols) * ((M + 127) / 128);
-    p.splits = prefill_splits(tiles, K / 64, sms);
-    if (p.splits > 1 && (size_t)tiles * sizeof(uint32_t) > kCounterBytes) p.splits = 1;
-    if (p.splits > 1) {
-      err = get_scratch(dev, stream, (size_t)tiles * p.splits * kPreSplitBytes, &p.counters, &p.partial);
-      if (err != MARLIN_HIP_OK) {
-        if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-        return err;
-      }
-    }
-    hipError_t e = launch_prefill(p, groupsize != -1, stream);
-    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-    if (e != hipSuccess) {
-      set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
-      return MARLIN_HIP_ERR_LAUNCH;
-    }
-    return MARLIN_HIP_OK;
-  }
-  Plan plan = plan_for(M, N, K, sms);
-  GemmArgs a;
-  a.A = static_cast<const _Float16*>(A);
-  a.B = B;
-  a.meta = meta;
-  a.s = static_cast<const _Float16*>(s);
-  a.C = static_cast<_Float16*>(C);
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  a.splits = plan.splits;
-  a.partial = nullptr;
-  a.counters = nullptr;
-  err = get_zeros(dev, &a.zeros);
-  if (err != MARLIN_HIP_OK) {
-    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-    return err;
-  }
-  const int chunks = N / 64;
-  if (plan.splits > 1) {
-    if ((size_t)chunks * plan.ztiles * sizeof(int) > kCounterBytes) {
-      plan.splits = 1;
-      a.splits = 1;
-    } else {
-      err = get_scratch(dev, stream, (size_t)plan.splits * M * N * sizeof(float), &a.counters, &a.partial);
-      if (err != MARLIN_HIP_OK) {
-        if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-        return err;
-      }
-    }
-  }
-  dim3 grid(chunks, plan.splits, plan.ztiles);
-  const bool grouped = groupsize != -1;
-  hipError_t e;
-  if (vf == VAL4 && mf == META4) e = launch_v<VAL4, META4>(a, plan.bb, grouped, grid, stream);
-  else if (vf == VAL4) e = launch_v<VAL4, META3>(a, plan.bb, grouped, grid, stream);
-  else e = launch_v<VAL3, META4>(a, plan.bb, grouped, grid, stream);
-  if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
-  if (e != hipSuccess) {
-    set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
-    return MARLIN_HIP_ERR_LAUNCH;
-  }
-  return MARLIN_HIP_OK;
-}
-
-// ---- lane-native layout (sm24_native.h): repack, unpack, GEMM ----
-
-int check_native_shape(int N, int K, int groupsize) {
-  if (N <= 0 || K <= 0 || N % 64 != 0 || K % 256 != 0 || !(groupsize == -1 || groupsize == 64)) {
-    set_error("marlin_hip: the native layout needs N % 64 == 0, K % 256 == 0 and groupsize 64 (dense 128) or -1");
-    return MARLIN_HIP_ERR_PROB_SHAPE;
-  }
-  return MARLIN_HIP_OK;
-}
-
 // Sets `dev` current for the scope of a call and restores the caller's device.
 struct DeviceScope {
   int prev = -1;
@@ -848,6 +726,197 @@ struct DeviceScope {
     if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
   }
 };
+
+enum : int { KERNEL_DECODE = 0, KERNEL_PREFILL = 1, KERNEL_GENERAL = 2 };
+
+// The kernel a call on the reference layout runs (after 3-bit operands at large M are
+// expanded to 4 bits): the decode kernel up to 32 rows, and below the large-M
+// kernel's threshold up to 96 rows as consecutive launches of <= 32 rows (measured
+// on the Llama-2-7B shapes: o at M = 64 17.8 against 28.8 us, down at M = 96 40.5
+// against 49.7 us for the general kernel); the large-M kernel where it fits; the
+// general kernel otherwise.
+int kernel_for(int M, int N, int K) {
+  const bool chunked = M > kDecodeMaxM && M <= kDecodeChunkMaxM && !prefill_fits(M, N, K, VAL4, META4);
+  if (M <= kDecodeMaxM || chunked) return KERNEL_DECODE;
+  return prefill_fits(M, N, K, VAL4, META4) ? KERNEL_PREFILL : KERNEL_GENERAL;
+}
+
+// What run() launches for a 4-bit call when nothing limits its scratch:
+// out = {kernel, workgroups of the first launch, threads per workgroup, K splits of
+// the first launch, launches}.
+void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
+  const int kernel = kernel_for(M, N, K);
+  out[0] = kernel;
+  if (kernel == KERNEL_DECODE) {
+    const int mc = M < kDecodeMaxM ? M : kDecodeMaxM;
+    DecodeShape d = decode_shape(mc, N, K, sms);
+    if (noalloc) decode_unsplit(d, K);
+    out[1] = N / d.tc * d.splits;
+    out[2] = 64 * d.nw;
+    out[3] = d.splits;
+    out[4] = (M + kDecodeMaxM - 1) / kDecodeMaxM;
+  } else if (kernel == KERNEL_PREFILL) {
+    const int tiles = (N / kPreTileCols) * ((M + 127) / 128);
+    int splits = noalloc ? 1 : prefill_splits(tiles, K / 64, sms);
+    if (splits > 1 && (size_t)tiles * sizeof(uint32_t) > kCounterBytes) splits = 1;
+    out[1] = tiles * splits;
+    out[2] = kPreThreads;
+    out[3] = splits;
+    out[4] = 1;
+  } else {
+    Plan plan = plan_for(M, N, K, sms);
+    if (noalloc || (size_t)(N / 64) * plan.ztiles * sizeof(int) > kCounterBytes) plan.splits = 1;
+    out[1] = (N / 64) * plan.splits * plan.ztiles;
+    out[2] = 64 * (plan.bb == 1 ? 8 : 4);
+    out[3] = plan.splits;
+    out[4] = 1;
+  }
+}
+
+int launch_error(hipError_t e) {
+  if (e == hipSuccess) return MARLIN_HIP_OK;
+  set_error(std::string("marlin_hip: kernel launch failed: ") + hipGetErrorString(e));
+  return MARLIN_HIP_ERR_LAUNCH;
+}
+
+// One GEMM call on the reference layout (or a 3-bit variant of it).  With `noalloc`
+// the call allocates nothing: it never splits K (so it needs no partials or
+// counters) and never stages operands (3-bit operands are refused), and its only
+// scratch is the static zero block.
+int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C, void* s, int prob_m,
+        int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream, int thread_k, int thread_m,
+        int sms, bool noalloc = false) {
+  int err = validate(prob_m, prob_n, prob_k, groupsize, thread_k, thread_m);
+  if (err != MARLIN_HIP_OK) return err;
+  if (prob_m == 0 || prob_n == 0 || prob_k == 0) return MARLIN_HIP_OK;
+  // The 64-column chunk and 32-deep k-block of the packed layouts (and 128-deep
+  // scale groups) are this implementation's own granularity.
+  if (prob_m % 64 != 0 || prob_k % 32 != 0 || (groupsize != -1 && prob_k % 128 != 0)) {
+    set_error("marlin_hip: N must be a multiple of 64 and K of 32 (128 when grouped)");
+    return MARLIN_HIP_ERR_PROB_SHAPE;
+  }
+  if (noalloc && (vf != VAL4 || mf != META4)) {
+    set_error("marlin_hip: the no-allocation entry point takes 4-bit values and metadata only");
+    return MARLIN_HIP_ERR_KERN_SHAPE;
+  }
+  DeviceScope scope(dev);
+  if (!scope.ok) return MARLIN_HIP_ERR_LAUNCH;
+  if (sms <= 0) {
+    if (hipDeviceGetAttribute(&sms, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || sms <= 0)
+      sms = 256;
+  }
+  const int M = prob_n, N = prob_m, K = prob_k;
+  const _Float16* zeros = nullptr;
+  err = get_zeros(dev, stream, &zeros);
+  if (err != MARLIN_HIP_OK) return err;
+  if (kernel_for(M, N, K) == KERNEL_DECODE) {
+    for (int r0 = 0; r0 < M; r0 += kDecodeMaxM) {
+      const int mc = M - r0 < kDecodeMaxM ? M - r0 : kDecodeMaxM;
+      GemmArgs d{};
+      d.A = static_cast<const _Float16*>(A) + (size_t)r0 * K;
+      d.B = B;
+      d.meta = meta;
+      d.s = static_cast<const _Float16*>(s);
+      d.C = static_cast<_Float16*>(C) + (size_t)r0 * N;
+      d.zeros = zeros;
+      d.M = mc;
+      d.N = N;
+      d.K = K;
+      DecodeShape shape = decode_shape(mc, N, K, sms);
+      if (noalloc) decode_unsplit(shape, K);
+      if (shape.splits > 1) {
+        const int rows = decode_batch(mc) > 16 ? decode_batch(mc) : 16;
+        err = get_scratch(dev, stream, (size_t)(N / shape.tc) * shape.splits * rows * shape.tc * sizeof(float),
+                          &d.counters, &d.partial);
+        if (err != MARLIN_HIP_OK) return err;
+        if (!d.counters) decode_unsplit(shape, K);  // capturing, and this stream has no scratch yet
+      }
+      d.splits = shape.splits;
+      err = launch_error(launch_decode(d, shape, vf, mf, groupsize != -1, stream));
+      if (err != MARLIN_HIP_OK) return err;
+    }
+    return MARLIN_HIP_OK;
+  }
+  if (prefill_fits(M, N, K, VAL4, META4) && (vf != VAL4 || mf != META4)) {
+    // 3-bit values or metadata at large M: expand them into the 4-bit layouts on this
+    // stream, then the large-M kernel reads the expanded copy.
+    const size_t vbytes = vf == VAL3 ? (size_t)K * N / 4 : 0, mbytes = mf == META3 ? (size_t)K * N / 8 : 0;
+    void* stage = nullptr;
+    err = get_stage(dev, stream, vbytes + mbytes, &stage);
+    if (err != MARLIN_HIP_OK) return err;
+    if (vf == VAL3) {
+      const long long quads = (long long)K * N / 64;
+      hipLaunchKernelGGL(w3_to_w4_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                         static_cast<const uint32_t*>(B), static_cast<u32x4*>(stage), quads);
+      B = stage;
+    }
+    if (mf == META3) {
+      void* m4 = static_cast<char*>(stage) + vbytes;
+      err = marlin_hip_meta3_unpack(meta, m4, (long long)K * N / 8 / 4 * 3 / 4, dev, stream);
+      if (err != MARLIN_HIP_OK) return err;
+      meta = m4;
+    }
+    vf = VAL4;
+    mf = META4;
+  }
+  if (prefill_fits(M, N, K, vf, mf)) {
+    GemmArgs p{};
+    p.A = static_cast<const _Float16*>(A);
+    p.B = B;
+    p.meta = meta;
+    p.s = static_cast<const _Float16*>(s);
+    p.C = static_cast<_Float16*>(C);
+    p.zeros = zeros;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    const int tiles = (N / kPreTileCols) * ((M + 127) / 128);
+    p.splits = noalloc ? 1 : prefill_splits(tiles, K / 64, sms);
+    if (p.splits > 1 && (size_t)tiles * sizeof(uint32_t) > kCounterBytes) p.splits = 1;
+    if (p.splits > 1) {
+      err = get_scratch(dev, stream, (size_t)tiles * p.splits * kPreSplitBytes, &p.counters, &p.partial);
+      if (err != MARLIN_HIP_OK) return err;
+      if (!p.counters) p.splits = 1;
+    }
+    return launch_error(launch_prefill(p, groupsize != -1, stream));
+  }
+  Plan plan = plan_for(M, N, K, sms);
+  const int chunks = N / 64;
+  if (noalloc || (size_t)chunks * plan.ztiles * sizeof(int) > kCounterBytes) plan.splits = 1;
+  GemmArgs a{};
+  a.A = static_cast<const _Float16*>(A);
+  a.B = B;
+  a.meta = meta;
+  a.s = static_cast<const _Float16*>(s);
+  a.C = static_cast<_Float16*>(C);
+  a.zeros = zeros;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  if (plan.splits > 1) {
+    err = get_scratch(dev, stream, (size_t)plan.splits * M * N * sizeof(float), &a.counters, &a.partial);
+    if (err != MARLIN_HIP_OK) return err;
+    if (!a.counters) plan.splits = 1;
+  }
+  a.splits = plan.splits;
+  dim3 grid(chunks, plan.splits, plan.ztiles);
+  const bool grouped = groupsize != -1;
+  hipError_t e;
+  if (vf == VAL4 && mf == META4) e = launch_v<VAL4, META4>(a, plan.bb, grouped, grid, stream);
+  else if (vf == VAL4) e = launch_v<VAL4, META3>(a, plan.bb, grouped, grid, stream);
+  else e = launch_v<VAL3, META4>(a, plan.bb, grouped, grid, stream);
+  return launch_error(e);
+}
+
+// ---- lane-native layout (sm24_native.h): repack, unpack, GEMM ----
+
+int check_native_shape(int N, int K, int groupsize) {
+  if (N <= 0 || K <= 0 || N % 64 != 0 || K % 256 != 0 || !(groupsize == -1 || groupsize == 64)) {
+    set_error("marlin_hip: the native layout needs N % 64 == 0, K % 256 == 0 and groupsize 64 (dense 128) or -1");
+    return MARLIN_HIP_ERR_PROB_SHAPE;
+  }
+  return MARLIN_HIP_OK;
+}
 
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
@@ -991,13 +1060,11 @@ int run_native(const void* A, const void* W, const void* X, void* C, const void*
   const NativeShape sh = native_shape(MB, N, K, sms);
   const int ncb = sh.ncb;
   a.splits = sh.splits;
+  if (a.splits > 1 && (size_t)(N / (16 * ncb)) * sizeof(uint32_t) > kCounterBytes) a.splits = 1;
   if (a.splits > 1) {
-    if ((size_t)(N / (16 * ncb)) * sizeof(uint32_t) > kCounterBytes) {
-      set_error("marlin_hip: N too large for the native kernel's split-K counters");
-      return MARLIN_HIP_ERR_PROB_SHAPE;
-    }
     err = get_scratch(dev, stream, (size_t)(N / 16) * a.splits * MB * 16 * sizeof(float), &a.counters, &a.partial);
     if (err != MARLIN_HIP_OK) return err;
+    if (!a.counters) a.splits = 1;  // capturing, and this stream has no scratch yet
   }
   const size_t act = (size_t)4 * MB * 512;  // a staging slot per wave
   const size_t red = (size_t)4 * ncb * MB * 16 * sizeof(float);
@@ -1060,6 +1127,23 @@ int marlin_hip_mul_2_4(const void* A, const void* B, const void* meta, void* C, 
   (void)max_par;
   return sm24::run(sm24::VAL4, sm24::META4, A, B, meta, C, s, prob_m, prob_n, prob_k, groupsize, dev, stream,
                    thread_k, thread_m, sms);
+}
+
+int marlin_hip_plan(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, int thread_m, int sms,
+                    int noalloc, int* out) {
+  int err = sm24::validate(prob_m, prob_n, prob_k, groupsize, thread_k, thread_m);
+  if (err != MARLIN_HIP_OK) return err;
+  if (prob_m % 64 != 0 || prob_k % 32 != 0 || (groupsize != -1 && prob_k % 128 != 0)) {
+    sm24::set_error("marlin_hip: N must be a multiple of 64 and K of 32 (128 when grouped)");
+    return MARLIN_HIP_ERR_PROB_SHAPE;
+  }
+  if (prob_m == 0 || prob_n == 0 || prob_k == 0) {
+    for (int i = 0; i < 5; i++) out[i] = 0;
+    out[0] = -1;
+    return MARLIN_HIP_OK;
+  }
+  sm24::describe(prob_n, prob_m, prob_k, sms > 0 ? sms : 256, noalloc != 0, out);
+  return MARLIN_HIP_OK;
 }
 
 int marlin_hip_mul_2_4_meta3(const void* A, const void* B, const void* meta3, void* C, void* s, int prob_m,

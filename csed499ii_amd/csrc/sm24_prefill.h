@@ -46,8 +46,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPreRows = 128;  // batch rows per tile
 constexpr int kPreChunks = 8;  // 64-column chunks per tile = waves per workgroup
-static_assert(64 * kPreChunks == kPreTileCols, "tile width");
-constexpr int kPreThreads = 64 * kPreChunks;
+static_assert(64 * kPreChunks == kPreTileCols && kPreThreads == 64 * kPreChunks, "tile width");
 constexpr int kPreRing = 4;                        // k-steps resident in LDS
 constexpr int kPreActB = kPreRows * 128;           // activation bytes of one k-step
 // Weight side of one k-step, per wave (one chunk): packed values of both k-blocks

@@ -29,6 +29,7 @@ from ._semi_structured_conversions import (
 
 __all__ = [
     "mul_2_4",
+    "plan_2_4",
     "mul_2_4_meta3",
     "mul_2_4_w3",
     "Layer_2_4",
@@ -61,7 +62,9 @@ def _check_operands(A, B, meta, C, s, workspace, b_elems: int, b_dtype: torch.dt
     """Device, dtype, contiguity and size checks.  The reference binding checks none of
     these (it hands raw pointers to the kernel); here a mismatch raises instead of
     reading or writing out of bounds on the GPU."""
-    tensors = {"A": A, "B": B, "meta": meta, "C": C, "s": s, "workspace": workspace}
+    tensors = {"A": A, "B": B, "meta": meta, "C": C, "s": s}
+    if workspace is not None:
+        tensors["workspace"] = workspace
     for name, t in tensors.items():
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor")
@@ -100,7 +103,7 @@ def _groupsize_and_checks(A, C, s, workspace, max_par):
     groupsize = -1 if s.size(0) == 1 else prob_k // 2 // s.size(0)
     if groupsize != -1 and groupsize * s.size(0) != prob_k // 2:
         raise RuntimeError(f"k={prob_k} not compatible with {s.size(0)} groups.")
-    if workspace.numel() < prob_m // 128 * max_par:
+    if workspace is not None and workspace.numel() < prob_m // 128 * max_par:
         raise RuntimeError(f"workspace must be of size at least {prob_m // 128 * max_par}.")
     return prob_m, prob_n, prob_k, groupsize
 
@@ -140,13 +143,33 @@ def mul_2_4(A, B, meta, C, s, workspace, thread_k=-1, thread_m=-1, sms=-1, max_p
     (``K*N/16`` elements, ``Layer_2_4.pack`` layout); ``meta`` int16 2:4 metadata
     (``K*N/16`` elements); ``C`` fp16 ``[M, N]``, overwritten; ``s`` fp16 scales
     ``[K/128, N]`` or ``[1, N]``; ``workspace`` int32 with at least ``N/128*max_par``
-    elements (kept for compatibility; it is not written and need not be zeroed).
+    elements (kept for compatibility; it is neither read nor written: the library
+    keeps its split-K scratch per device and stream, so calls on different streams
+    may overlap).
     ``thread_k``/``thread_m`` are validated like the reference's tile choices;
     ``sms`` is the number of compute units to plan for (-1: all).  Asynchronous on
     the current stream of ``A``'s device.
     """
     _call("marlin_hip_mul_2_4", A, B, meta, C, s, workspace, thread_k, thread_m, sms, max_par,
           lambda k, n: k * n // 16, torch.int32, lambda k, n: k * n // 16, torch.int16)
+
+
+_KERNELS = {-1: None, 0: "decode", 1: "large_m", 2: "general"}
+
+
+def plan_2_4(M: int, K: int, N: int, groupsize: int = 128, thread_k: int = -1, thread_m: int = -1, sms: int = -1,
+             noalloc: bool = False) -> dict:
+    """The launch plan of a ``mul_2_4`` call on ``A [M, K]`` and an ``N``-column weight
+    (``noalloc=True``: planned without K splits), computed on the host without a GPU
+    (``marlin_hip_plan``): kernel, workgroups and K splits of the first launch,
+    threads per workgroup and launches.  ``splits > 1`` means the call uses its
+    stream's split-K scratch.  Raises like ``mul_2_4`` for shapes it refuses."""
+    out = (ctypes.c_int * 5)()
+    g = groupsize // 2 if groupsize != -1 else -1
+    err = _lib.load().marlin_hip_plan(N, M, K, g, thread_k, thread_m, sms, int(noalloc), out)
+    _raise_for(err, N, M, K, thread_k, thread_m, g)
+    return {"kernel": _KERNELS[out[0]], "workgroups": out[1], "threads": out[2], "splits": out[3],
+            "launches": out[4]}
 
 
 def mul_2_4_meta3(A, B, meta3, C, s, workspace, thread_k=-1, thread_m=-1, sms=-1, max_par=16):
@@ -485,6 +508,15 @@ class Layer_2_4(nn.Module):
         self.register_buffer("s", torch.empty((self.k // groupsize, self.n), dtype=torch.half))
         # 128 is the reference's minimum tile_n and 16 its default max_par.
         self.register_buffer("workspace", torch.zeros(self.n // 128 * 16, dtype=torch.int32), persistent=False)
+        self.register_load_state_dict_post_hook(Layer_2_4._refresh_native)
+
+    @staticmethod
+    def _refresh_native(module, incompatible_keys):
+        """After ``load_state_dict`` (in place or with ``assign=True``) a lane-native copy
+        made by :meth:`to_native` holds the old weight: rebuild it from the loaded
+        buffers."""
+        if getattr(module, "Bn", None) is not None:
+            module.to_native()
 
     def forward(self, A):
         C = torch.empty(A.shape[:-1] + (self.s.shape[1],), dtype=A.dtype, device=A.device)
@@ -503,7 +535,9 @@ class Layer_2_4(nn.Module):
         batches of at most 16 rows, which ``forward`` then runs on
         :func:`mul_2_4_native`; larger batches keep using the pack() buffers, which
         stay the module's ``state_dict``.  Needs ``infeatures % 256 == 0``; the copy
-        is as large as the packed weight.  Returns the module."""
+        is as large as the packed weight.  ``pack`` and ``load_state_dict`` rebuild
+        the copy; after an in-place edit of ``B``, ``meta`` or ``s`` call
+        ``to_native()`` again.  Returns the module."""
         Bn, metan, sn = pack_native(self.B, self.meta, self.s)
         self.register_buffer("Bn", Bn, persistent=False)
         self.register_buffer("metan", metan, persistent=False)

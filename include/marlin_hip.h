@@ -16,15 +16,21 @@
  * s (K/128 or 1)*N halves.
  *
  * The planner may split K (decode calls at wide N or long K, large-M calls with few
- * column tiles); the split-K scratch (fp32 partials and arrival counters) is
- * uncached device memory that the library allocates once per device, grows on
- * demand outside stream capture (a grow during capture is refused with code 3) and
- * never frees.  The counters are
- * zeroed at allocation and each is returned to zero by the last workgroup that
- * arrives on it, so no buffer needs to be zeroed by the caller.  The scratch is
- * shared by all streams of a device: split-K calls that overlap in time on one
- * device race (serialise them on one stream, as with the reference's shared
- * workspace).
+ * column tiles, lane-native calls at 5-16 rows whose tiles cover too few compute
+ * units, and at 2-4 rows when K >= 16384).  The split-K scratch (fp32 partials and
+ * arrival counters) is uncached device memory that the library allocates per
+ * (device, stream), grows on demand and never frees; the operand staging buffer of
+ * the 3-bit variants at large M and of the lane-native layout above 16 rows is kept
+ * the same way.  Calls on different streams therefore never share a buffer and may
+ * overlap in time; calls on one stream are ordered.  `workspace` is not used (the
+ * reference keeps its split-K locks there, common/mem.h:111-142).
+ * The counters are zeroed at allocation and each is returned to zero by the last
+ * workgroup that arrives on it, so no buffer needs to be zeroed by the caller.
+ * During stream capture nothing can be allocated: a call whose stream has no large
+ * enough scratch yet then runs without splitting K (same result within the GEMM
+ * tolerance, a different summation order), and one that needs a larger staging
+ * buffer fails with code 3; an eager call of the same shape on the capturing stream
+ * before the capture sizes both.
  */
 #ifndef MARLIN_HIP_H
 #define MARLIN_HIP_H
@@ -46,12 +52,25 @@ enum {
  * Replaces marlin::marlin_cuda_2_4 (kernel_experiments/sparse_marlin/src/marlin/
  * marlin_cuda_kernel_nm.cu:751-755), same parameter order and meaning.
  * `workspace` and `max_par` are accepted for signature compatibility; this library
- * keeps its own zero-initialised scratch, so the caller's workspace need not be
- * zeroed.  thread_k/thread_m are validated exactly as the reference does. */
+ * keeps its own scratch per (device, stream), so the caller's workspace is neither
+ * read nor written.  thread_k/thread_m are validated exactly as the reference does
+ * (the kernel and tile are then chosen by this library's planner). */
 int marlin_hip_mul_2_4(const void* A, const void* B, const void* meta, void* C, void* s,
                        int prob_m, int prob_n, int prob_k, void* workspace, int groupsize,
                        int dev, hipStream_t stream, int thread_k, int thread_m, int sms,
                        int max_par);
+
+/* The launch plan of a marlin_hip_mul_2_4 call (noalloc = 0; noalloc = 1: the same
+ * call planned without K splits), computed on the host without a GPU:
+ * out[0] kernel (0 decode, 1 large-M, 2 general; -1 for an empty problem),
+ * out[1] workgroups of the first launch, out[2] threads per workgroup, out[3] K
+ * splits of the first launch (> 1: the call uses its stream's split-K scratch),
+ * out[4] launches.  sms <= 0 plans for 256 compute units.  Returns the codes of
+ * marlin_hip_mul_2_4's shape checks.  No counterpart in the reference (its host
+ * dispatch, marlin_cuda_kernel_nm.cu:763-806, is not exposed); it lets a caller see
+ * which calls split K and lets a benchmark launch an empty kernel on the same grid. */
+int marlin_hip_plan(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, int thread_m, int sms,
+                    int noalloc, int* out);
 
 /* Same GEMM with 3-bit-compressed metadata (48 uint32 per 64-word group) as
  * produced by marlin_hip_meta3_pack.  Replaces the generated
@@ -107,9 +126,10 @@ int marlin_hip_native_unpack(const void* Bn, const void* metan, const void* sn, 
 
 /* C[M,N] = A[M,K] * W[K,N] with W in the lane-native layout (same arguments as
  * marlin_hip_mul_2_4 where they exist; automatic tiles only).  M <= 16 runs the
- * native decode kernel (at M = 2..16 and K >= 16384 split in two along K, through
- * the library's split-K scratch); larger M unpacks the weight into
- * the library's staging buffer on `stream` and runs the reference-layout kernels.
+ * native decode kernel (split along K at 2-4 rows when K >= 16384, and at 5-16 rows
+ * when the column tiles alone cover under 60 % of the compute units, through the
+ * stream's split-K scratch); larger M unpacks the weight into the stream's staging
+ * buffer and runs the reference-layout kernels.
  * No counterpart in the reference (see marlin_hip_native_pack). */
 int marlin_hip_mul_2_4_native(const void* A, const void* Bn, const void* metan, void* C, const void* sn,
                               int prob_m, int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream,

@@ -1,0 +1,25 @@
+/* C ABI of libmarlin_probe.so: measurement aids of bench.py's floor workload.  Not
+ * part of the GEMM library and with no counterpart in the reference.  Return codes:
+ * 0 ok, 1 bad argument, 3 HIP failure. */
+#ifndef MARLIN_PROBE_H
+#define MARLIN_PROBE_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Read `bytes` (a multiple of 16) from device pointer `p` with 16-byte loads on
+ * `blocks` workgroups of 256 threads; `sink` is a device uint32 that is written only
+ * in the (practically impossible) case that the XOR of all words is 0x9E3779B9. */
+int marlin_probe_read(const void* p, long long bytes, void* sink, int blocks, int dev, hipStream_t stream);
+
+/* An empty kernel on `blocks` workgroups of `threads` threads. */
+int marlin_probe_empty(int blocks, int threads, int dev, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MARLIN_PROBE_H */

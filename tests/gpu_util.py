@@ -52,3 +52,27 @@ def assert_close(C: np.ndarray, ref: np.ndarray, what: str = ""):
     assert rel <= REL_MAE, f"{what}: relative MAE {rel:.3e} > {REL_MAE}"
     assert mx <= MAX_REL, f"{what}: max error {mx:.3e} of max|ref| > {MAX_REL}"
     return rel, mx
+
+
+_WEIGHTS = {}
+
+
+def cached_weight(K: int, N: int, seed: int, device: str = "cuda:0"):
+    """One large packed weight at a time (device copy and host copy), kept between the
+    tests that use the same (K, N, seed) so that a Llama-2-70B weight is built once."""
+    from csed499ii_amd import synth
+
+    key = (K, N, seed)
+    if key not in _WEIGHTS:
+        _WEIGHTS.clear()
+        wt = synth.make_weight(K, N, seed, 128, device=device)
+        _WEIGHTS[key] = (wt, to_cpu(wt))
+    return _WEIGHTS[key]
+
+
+def check_slices(C, A_np: np.ndarray, t: dict, starts, nc: int, what: str):
+    """Compare columns [64*c0, 64*(c0+nc)) of the GPU output C (all rows) with the
+    oracle on the same column slice of the packed weight, for every c0 in starts."""
+    for c0 in starts:
+        ref = oracle_gemm(A_np, slice_cols(t, c0, nc))
+        assert_close(C[:, 64 * c0:64 * (c0 + nc)].cpu().numpy(), ref, f"{what} slice {c0}")

@@ -84,3 +84,43 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load()
+
+
+def test_plan_without_gpu(built_lib):
+    """marlin_hip_plan is host-only: the decode sweep's plans (the split-K choices that
+    decide which calls use a stream's scratch), the large-M kernel at prefill sizes,
+    and the no-allocation variant, which never splits K."""
+    from csed499ii_amd import marlin
+
+    p = marlin.plan_2_4(1, 4096, 4096)
+    assert p["kernel"] == "decode" and p["splits"] == 1 and p["launches"] == 1
+    assert p["workgroups"] * (p["threads"] // 64) > 0
+    p = marlin.plan_2_4(16, 4096, 22016)  # wide N from 8 rows: 64-column tiles split in two
+    assert p["kernel"] == "decode" and p["splits"] == 2 and p["workgroups"] == 22016 // 64 * 2
+    assert marlin.plan_2_4(16, 4096, 22016, noalloc=True)["splits"] == 1
+    assert marlin.plan_2_4(4, 8192, 8192)["splits"] == 1  # 16-column tiles fill the CUs
+    assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4  # long K, wider N: K split four ways
+    p = marlin.plan_2_4(64, 4096, 4096)  # below the large-M threshold: two decode launches
+    assert p["kernel"] == "decode" and p["launches"] == 2
+    for M in (512, 4096):
+        p = marlin.plan_2_4(M, 8192, 57344)
+        assert p["kernel"] == "large_m" and p["threads"] == 512
+        assert p["workgroups"] == 57344 // 512 * (M // 128) * p["splits"]
+    assert marlin.plan_2_4(512, 8192, 10240)["splits"] > 1  # few tiles: split K
+    assert marlin.plan_2_4(512, 8192, 10240, noalloc=True)["splits"] == 1
+    assert marlin.plan_2_4(300, 4096, 768)["kernel"] == "general"  # N % 512 != 0
+    with pytest.raises(RuntimeError, match="not compatible"):
+        marlin.plan_2_4(16, 1000, 512)
+    assert marlin.plan_2_4(0, 4096, 4096)["kernel"] is None
+
+
+def test_probe_library_exports(built_lib):
+    """bench.py's measurement library exports what include/marlin_probe.h declares."""
+    from csed499ii_amd import build
+
+    header = (HEADER.parent / "marlin_probe.h").read_text()
+    declared = set(re.findall(r"^\s*int\s+(marlin_probe_\w+)\s*\(", header, re.M))
+    assert declared == {"marlin_probe_read", "marlin_probe_empty"}
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.PROBE_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    assert declared <= set(re.findall(r"\bT\s+(marlin_probe_\w+)", out))

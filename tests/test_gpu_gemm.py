@@ -113,7 +113,7 @@ def test_config1_and_decode_o_proj(M):
 
 
 @pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 22016), (11008, 4096), (4096, 4096)])
-@pytest.mark.parametrize("M", [1, 3, 8, 16, 24, 32, 64, 90])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16, 24, 32, 64, 90])
 def test_decode_sweep_full_size_slices(K, N, M):
     """Full-width calls (every decode tile width and padded batch), checked on
     column slices; repeated calls must be bit-identical (a race between the LDS

@@ -55,7 +55,7 @@ def test_meta3_gemm_equals_baseline_bit_exact(M, N, K, g):
 
 
 @pytest.mark.parametrize("M", [1, 16, 32, 256])
-@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 12288), (11008, 4096)])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 12288), (4096, 22016), (11008, 4096)])
 def test_w3_gemm_config4(M, K, N):
     """Benchmark config 4: 3-bit values, Llama-2-7B shapes, M in {1, 16, 256}."""
     wt = synth.make_weight(K, N, 4 + K + N, 128, bits=3, device=DEV)
