@@ -23,6 +23,7 @@ _ll = ctypes.c_longlong
 #: name -> (restype, argtypes); must match include/marlin_hip.h
 SIGNATURES = {
     "marlin_hip_mul_2_4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),
+    "marlin_hip_mul_2_4_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i]),
     "marlin_hip_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
     "marlin_hip_mul_2_4_meta3": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),
     "marlin_hip_mul_2_4_w3": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),

@@ -322,7 +322,7 @@ bool capturing(hipStream_t stream) {
 // kernels read in place of activation rows that do not exist (rows past M, k-blocks
 // past K).  Every device holds its own copy from module load until the process ends;
 // no kernel writes it, so calls on any stream may share it.  It is all the scratch
-// that a call planned without K splits needs.
+// that marlin_hip_mul_2_4_noalloc needs, because that entry point never splits K.
 constexpr size_t kScratchBytes = 256;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -1144,6 +1144,13 @@ int marlin_hip_plan(int prob_m, int prob_n, int prob_k, int groupsize, int threa
   }
   sm24::describe(prob_n, prob_m, prob_k, sms > 0 ? sms : 256, noalloc != 0, out);
   return MARLIN_HIP_OK;
+}
+
+int marlin_hip_mul_2_4_noalloc(const void* A, const void* B, const void* meta, void* C, const void* s,
+                               int prob_m, int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream,
+                               int thread_k, int thread_m, int sms) {
+  return sm24::run(sm24::VAL4, sm24::META4, A, B, meta, C, const_cast<void*>(s), prob_m, prob_n, prob_k,
+                   groupsize, dev, stream, thread_k, thread_m, sms, /*noalloc=*/true);
 }
 
 int marlin_hip_mul_2_4_meta3(const void* A, const void* B, const void* meta3, void* C, void* s, int prob_m,

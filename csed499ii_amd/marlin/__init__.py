@@ -29,6 +29,7 @@ from ._semi_structured_conversions import (
 
 __all__ = [
     "mul_2_4",
+    "mul_2_4_noalloc",
     "plan_2_4",
     "mul_2_4_meta3",
     "mul_2_4_w3",
@@ -160,7 +161,7 @@ _KERNELS = {-1: None, 0: "decode", 1: "large_m", 2: "general"}
 def plan_2_4(M: int, K: int, N: int, groupsize: int = 128, thread_k: int = -1, thread_m: int = -1, sms: int = -1,
              noalloc: bool = False) -> dict:
     """The launch plan of a ``mul_2_4`` call on ``A [M, K]`` and an ``N``-column weight
-    (``noalloc=True``: planned without K splits), computed on the host without a GPU
+    (``noalloc=True``: of ``mul_2_4_noalloc``), computed on the host without a GPU
     (``marlin_hip_plan``): kernel, workgroups and K splits of the first launch,
     threads per workgroup and launches.  ``splits > 1`` means the call uses its
     stream's split-K scratch.  Raises like ``mul_2_4`` for shapes it refuses."""
@@ -170,6 +171,20 @@ def plan_2_4(M: int, K: int, N: int, groupsize: int = 128, thread_k: int = -1, t
     _raise_for(err, N, M, K, thread_k, thread_m, g)
     return {"kernel": _KERNELS[out[0]], "workgroups": out[1], "threads": out[2], "splits": out[3],
             "launches": out[4]}
+
+
+def mul_2_4_noalloc(A, B, meta, C, s, thread_k=-1, thread_m=-1, sms=-1):
+    """``mul_2_4`` through ``marlin_hip_mul_2_4_noalloc``: the same product without any
+    device allocation (it never splits K, so it needs no split-K scratch; safe to
+    capture on a stream that has never run a call).  No reference counterpart."""
+    lib = _lib.load()
+    prob_m, prob_n, prob_k, groupsize = _groupsize_and_checks(A, C, s, None, 0)
+    _check_operands(A, B, meta, C, s, None, prob_k * prob_m // 16, torch.int32, prob_k * prob_m // 16, torch.int16)
+    stream = torch.cuda.current_stream(A.device).cuda_stream
+    err = lib.marlin_hip_mul_2_4_noalloc(_ptr(A), _ptr(B), _ptr(meta), _ptr(C), _ptr(s), prob_m, prob_n, prob_k,
+                                         groupsize, A.get_device(), ctypes.c_void_p(stream), thread_k, thread_m,
+                                         sms)
+    _raise_for(err, prob_m, prob_n, prob_k, thread_k, thread_m, groupsize)
 
 
 def mul_2_4_meta3(A, B, meta3, C, s, workspace, thread_k=-1, thread_m=-1, sms=-1, max_par=16):

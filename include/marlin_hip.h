@@ -60,8 +60,22 @@ int marlin_hip_mul_2_4(const void* A, const void* B, const void* meta, void* C, 
                        int dev, hipStream_t stream, int thread_k, int thread_m, int sms,
                        int max_par);
 
-/* The launch plan of a marlin_hip_mul_2_4 call (noalloc = 0; noalloc = 1: the same
- * call planned without K splits), computed on the host without a GPU:
+/* marlin_hip_mul_2_4 without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory at call time (code under HIP
+ * graph capture on a stream that has no scratch yet, serving loops and harnesses
+ * that forbid hipMalloc).  It never splits K and never stages operands, so the only
+ * scratch its kernels use is the library's static 256-byte zero block (a
+ * `__device__` array that every device holds from module load to process end); no
+ * problem size needs more, and shapes are refused only by marlin_hip_mul_2_4's
+ * rules.  Same arguments and return codes as marlin_hip_mul_2_4 without workspace
+ * and max_par.  The zero block is read-only, so overlapping calls on one device do
+ * not race on it. */
+int marlin_hip_mul_2_4_noalloc(const void* A, const void* B, const void* meta, void* C, const void* s,
+                               int prob_m, int prob_n, int prob_k, int groupsize, int dev, hipStream_t stream,
+                               int thread_k, int thread_m, int sms);
+
+/* The launch plan of a marlin_hip_mul_2_4 call (noalloc = 0) or of a
+ * marlin_hip_mul_2_4_noalloc call (noalloc = 1), computed on the host without a GPU:
  * out[0] kernel (0 decode, 1 large-M, 2 general; -1 for an empty problem),
  * out[1] workgroups of the first launch, out[2] threads per workgroup, out[3] K
  * splits of the first launch (> 1: the call uses its stream's split-K scratch),

@@ -114,6 +114,17 @@ def test_plan_without_gpu(built_lib):
     assert marlin.plan_2_4(0, 4096, 4096)["kernel"] is None
 
 
+def test_noalloc_host_validation(built_lib):
+    """The no-allocation entry point refuses what mul_2_4 refuses, before any launch."""
+    null = ctypes.c_void_p(0)
+    assert built_lib.marlin_hip_mul_2_4_noalloc(null, null, null, null, null, 512, 16, 1000, -1, 0, null, -1, -1,
+                                                -1) == _lib.ERR_PROB_SHAPE
+    assert built_lib.marlin_hip_mul_2_4_noalloc(null, null, null, null, null, 512, 32, 1024, -1, 0, null, 128, 128,
+                                                -1) == _lib.ERR_KERN_SHAPE
+    assert built_lib.marlin_hip_mul_2_4_noalloc(null, null, null, null, null, 512, 0, 1024, -1, 0, null, -1, -1,
+                                                -1) == _lib.OK
+
+
 def test_probe_library_exports(built_lib):
     """bench.py's measurement library exports what include/marlin_probe.h declares."""
     from csed499ii_amd import build
