@@ -93,19 +93,25 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int ngroups = (nkb + 3) >> 2;
   // Split-K: block b = z * ntiles + tile; split z covers stages [st0, st1) of the tile
   // (the host keeps splits <= the stage count).
+  // Without a split (the usual case) no division runs: a 64-bit or even a 32-bit
+  // division is a long scalar chain that every wave would pay before its first load.
   const int ntiles = N / TC;
   const int S = a.splits;
-  const int z = blockIdx.x / ntiles;
   const int nst_all = (nkb + KS - 1) / KS;
-  const int st0 = (int)(((long long)nst_all * z) / S);
-  const int nst = (int)(((long long)nst_all * (z + 1)) / S) - st0;  // stages of this split
+  int z = 0, st0 = 0, nst = nst_all;  // split z covers stages [st0, st0 + nst)
+  int tile = blockIdx.x;
+  if (S > 1) {  // uniform; nst_all * S is small, so 32 bits are exact
+    z = (int)((unsigned)blockIdx.x / (unsigned)ntiles);
+    tile -= z * ntiles;
+    st0 = (int)((unsigned)(nst_all * z) / (unsigned)S);
+    nst = (int)((unsigned)(nst_all * (z + 1)) / (unsigned)S) - st0;
+  }
   // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8 XCDs
   // (block b runs on XCD b % 8) and each XCD has its own L2.  The SUB = 64/TC tiles of
   // one 64-column chunk share 128-byte lines of metadata and scales (a tile's packed
   // values are whole lines), so they go to blocks b = 8*(SUB*q + s) + x, which all
   // sit on XCD x: each line is fetched from HBM once instead of once per tile.
   constexpr int SUB = 64 / TC;
-  int tile = blockIdx.x - z * ntiles;
   if constexpr (SUB > 1) {
     if (ntiles % (8 * SUB) == 0) {
       const int x = tile & 7, jx = tile >> 3;
