@@ -15,6 +15,9 @@ Other workloads: ``decode70b`` (the decode sweep on the Llama-2-70B shapes below
 lane-native layout of ``marlin.pack_native``), ``prefill`` (Llama-2-70B shapes, M in
 {512..4096}, TFLOP/s),
 ``w3`` (3-bit values, M in {1, 16, 256}), ``meta3`` (3-bit metadata, decode sweep),
+``dense`` (the decode sweep on the dense Marlin op ``marlin.mul``, GB/s on its K*N/2
+code bytes plus scales), ``floor`` (per decode-sweep call: a plain streaming read of
+its weight bytes and an empty kernel on its planned grid),
 ``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}; ``stack_native`` runs
 its M = 1 and M = 8 passes on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``copy`` (a plain
 1 GiB device copy: the calibration run for the HBM traffic counters), ``compare``
@@ -101,6 +104,8 @@ class Call:
 
     @property
     def wbytes(self):
+        if self.bits == "dense":
+            return synth.dense_weight_bytes(self.K, self.N, 128)
         b = synth.weight_bytes(self.K, self.N, self.bits, 128)
         if self.meta_key == "meta3":
             b -= self.K * self.N // 8 // 4  # metadata is 3/4 of the 4-bit size
@@ -127,6 +132,8 @@ def kernel_of(c) -> str:
     layout at M <= 16)."""
     if getattr(c, "native", False):
         return "sm24::sm24_native_decode_kernel"
+    if getattr(c, "bits", None) == "dense":
+        return "sm24::marlin_dense_kernel"
     min_m = 65 if c.N >= 16384 else (97 if c.N >= 4096 else 160)
     if c.M > 32 and c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"
@@ -135,8 +142,16 @@ def kernel_of(c) -> str:
     return "sm24::sm24_gemm_kernel"
 
 
+def dense_fn(A, B, meta, C, s, ws):
+    """Call-site adapter of the dense Marlin op (no metadata)."""
+    marlin.mul(A, B, C, s, ws)
+
+
 def make_copies(K, N, seed, bits, copies, device, meta3=False) -> WeightSet:
-    base = synth.make_weight(K, N, seed, 128, bits=bits, device=device)
+    if bits == "dense":
+        base = synth.make_dense_weight(K, N, seed, 128, device=device)
+    else:
+        base = synth.make_weight(K, N, seed, 128, bits=bits, device=device)
     if meta3:
         base["meta3"] = marlin.pack_meta3(base["meta"].reshape(-1))
     out = [base]
@@ -147,7 +162,8 @@ def make_copies(K, N, seed, bits, copies, device, meta3=False) -> WeightSet:
 
 def copies_for(K, N, bits) -> int:
     """Copies of one weight whose total exceeds the Infinity Cache by 25 %."""
-    return max(2, -(-int(MALL_BYTES * 1.25) // synth.weight_bytes(K, N, bits, 128)))
+    wb = synth.dense_weight_bytes(K, N, 128) if bits == "dense" else synth.weight_bytes(K, N, bits, 128)
+    return max(2, -(-int(MALL_BYTES * 1.25) // wb))
 
 
 _STREAM = None
@@ -461,6 +477,11 @@ def compare_libraries(device):
             row["ours_native_us"], _ = time_site(Call(name, K, N, M, WeightSet(nat_copies), A, native_fn))
             del nat_copies
         del ours
+        # the sibling op: this library's dense Marlin INT4 x FP16 GEMM (marlin.mul)
+        dense = Call(name, K, N, M, make_copies(K, N, synth.SEED_BASE + 51 + i, "dense",
+                                                copies_for(K, N, "dense") if decode else 1, device), A, dense_fn)
+        row["ours_dense_marlin_us"], _ = time_site(dense)
+        del dense
         for kind, key in (("dense", "dense_fp16_hipblaslt_us"), ("sparse", "sparse24_fp16_hipsparselt_us")):
             fp16_bytes = 2 * K * N // (1 if kind == "dense" else 2)
             copies = max(2, -(-int(MALL_BYTES * 1.25) // fp16_bytes)) if decode else 1
@@ -473,7 +494,8 @@ def compare_libraries(device):
                 row[key] = None
                 row[key.replace("_us", "_error")] = f"{type(e).__name__}: {str(e)[:160]}"
             torch.cuda.empty_cache()
-        for key in ("ours_us", "ours_native_us", "dense_fp16_hipblaslt_us", "sparse24_fp16_hipsparselt_us"):
+        for key in ("ours_us", "ours_native_us", "ours_dense_marlin_us", "dense_fp16_hipblaslt_us",
+                    "sparse24_fp16_hipsparselt_us"):
             if row.get(key) is not None:
                 row[key] = round(row[key], 2)
         rows.append(row)
@@ -483,24 +505,25 @@ def compare_libraries(device):
 def build_workload(args, device):
     wl = args.workload
     calls = []
-    if wl in ("decode", "decode70b", "meta3", "w3"):
+    if wl in ("decode", "decode70b", "meta3", "w3", "dense"):
         shapes = LLAMA70B if wl == "decode70b" else LLAMA7B
         Ms = [1, 2, 4, 8, 16] if wl != "w3" else [1, 16, 256]
-        bits = 3 if wl == "w3" else 4
+        bits = 3 if wl == "w3" else ("dense" if wl == "dense" else 4)
         weights = {}
         copies = {}
         for i, (name, K, N) in enumerate(shapes):
             copies[name] = copies_for(K, N, bits)
             weights[name] = make_copies(K, N, synth.SEED_BASE + 1 + i, bits, copies[name], device,
                                         meta3=(wl == "meta3"))
-        fn = marlin.mul_2_4_w3 if wl == "w3" else (marlin.mul_2_4_meta3 if wl == "meta3" else marlin.mul_2_4)
+        fn = {"w3": marlin.mul_2_4_w3, "meta3": marlin.mul_2_4_meta3, "dense": dense_fn}.get(wl, marlin.mul_2_4)
         meta_key = "meta3" if wl == "meta3" else "meta"
         for M in Ms:
             for name, K, N in shapes:
                 A = synth.make_activation(M, K, synth.SEED_BASE + M, device=device)
                 calls.append(Call(name, K, N, M, weights[name], A, fn, meta_key))
         cfg = {"workload": {"decode": "decode_sweep_llama2_7b", "decode70b": "decode_sweep_llama2_70b",
-                            "meta3": "decode_sweep_llama2_7b_meta3", "w3": "w3_values_llama2_7b"}[wl],
+                            "meta3": "decode_sweep_llama2_7b_meta3", "w3": "w3_values_llama2_7b",
+                            "dense": "dense_marlin_decode_sweep_llama2_7b"}[wl],
                "M": Ms, "shapes_KxN": [f"{K}x{N}" for _, K, N in shapes], "groupsize": 128,
                "weight_copies_made": copies}
     elif wl in ("native", "native70b"):
@@ -771,7 +794,7 @@ def main():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "stack",
+                   choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "dense", "stack",
                             "stack_native", "copy", "compare", "floor"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])

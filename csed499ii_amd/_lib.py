@@ -25,6 +25,7 @@ SIGNATURES = {
     "marlin_hip_mul_2_4": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),
     "marlin_hip_mul_2_4_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i]),
     "marlin_hip_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, ctypes.POINTER(_i)]),
+    "marlin_hip_mul": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),
     "marlin_hip_mul_2_4_meta3": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),
     "marlin_hip_mul_2_4_w3": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _i, _i, _i, _i]),
     "marlin_hip_meta3_pack": (_i, [_vp, _vp, _ll, _vp, _i, _vp]),

@@ -32,6 +32,7 @@
 
 #include "sm24_device.h"
 #include "sm24_decode.h"
+#include "sm24_host.h"
 #include "sm24_native.h"
 #include "../../include/marlin_hip.h"
 
@@ -360,7 +361,6 @@ int get_zeros(int dev, hipStream_t stream, const _Float16** out) {
   return MARLIN_HIP_OK;
 }
 
-constexpr size_t kCounterBytes = 64 * 1024;  // up to 16384 (chunk, batch-tile) counters
 
 // The split-K scratch of (dev, stream), grown to hold `partial_bytes` of partials.
 // A buffer cannot be allocated while the stream is being captured into a graph: then,
@@ -710,22 +710,6 @@ int validate(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, in
   return MARLIN_HIP_OK;
 }
 
-// Sets `dev` current for the scope of a call and restores the caller's device.
-struct DeviceScope {
-  int prev = -1;
-  bool ok = true;
-  explicit DeviceScope(int dev) {
-    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-    if (prev != dev && hipSetDevice(dev) != hipSuccess) {
-      set_error("marlin_hip: hipSetDevice failed");
-      ok = false;
-    }
-  }
-  ~DeviceScope() {
-    int cur = -1;
-    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-  }
-};
 
 enum : int { KERNEL_DECODE = 0, KERNEL_PREFILL = 1, KERNEL_GENERAL = 2 };
 

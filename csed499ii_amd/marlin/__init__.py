@@ -46,6 +46,9 @@ __all__ = [
     "pack_native",
     "unpack_native",
     "mul_2_4_native",
+    "mul",
+    "Layer",
+    "pack_dense",
 ]
 
 
@@ -60,10 +63,13 @@ def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
 
 def _check_operands(A, B, meta, C, s, workspace, b_elems: int, b_dtype: torch.dtype, meta_elems: int,
                     meta_dtype: torch.dtype):
-    """Device, dtype, contiguity and size checks.  The reference binding checks none of
-    these (it hands raw pointers to the kernel); here a mismatch raises instead of
-    reading or writing out of bounds on the GPU."""
-    tensors = {"A": A, "B": B, "meta": meta, "C": C, "s": s}
+    """Device, dtype, contiguity and size checks (``meta`` and ``workspace`` may be
+    None: the dense op has no metadata, the no-allocation op no workspace).  The
+    reference binding checks none of these (it hands raw pointers to the kernel);
+    here a mismatch raises instead of reading or writing out of bounds on the GPU."""
+    tensors = {"A": A, "B": B, "C": C, "s": s}
+    if meta is not None:
+        tensors["meta"] = meta
     if workspace is not None:
         tensors["workspace"] = workspace
     for name, t in tensors.items():
@@ -77,7 +83,7 @@ def _check_operands(A, B, meta, C, s, workspace, b_elems: int, b_dtype: torch.dt
             raise RuntimeError(f"{name} must be contiguous")
     for name, t, dt in (("A", A, torch.half), ("C", C, torch.half), ("s", s, torch.half),
                         ("B", B, b_dtype), ("meta", meta, meta_dtype)):
-        if t.dtype != dt:
+        if t is not None and t.dtype != dt:
             raise RuntimeError(f"{name} must be {dt}, got {t.dtype}")
     if A.dim() != 2 or C.dim() != 2 or s.dim() != 2:
         raise RuntimeError("A, C and s must be 2-dimensional")
@@ -89,7 +95,7 @@ def _check_operands(A, B, meta, C, s, workspace, b_elems: int, b_dtype: torch.dt
         raise RuntimeError(f"s has {s.shape[1]} columns, C has {N}")
     if B.numel() != b_elems:
         raise RuntimeError(f"B has {B.numel()} elements, expected {b_elems} for K={K}, N={N}")
-    if meta.numel() != meta_elems:
+    if meta is not None and meta.numel() != meta_elems:
         raise RuntimeError(f"meta has {meta.numel()} elements, expected {meta_elems} for K={K}, N={N}")
     for name, t in tensors.items():
         if t.numel() and t.data_ptr() % 16:
@@ -153,6 +159,37 @@ def mul_2_4(A, B, meta, C, s, workspace, thread_k=-1, thread_m=-1, sms=-1, max_p
     """
     _call("marlin_hip_mul_2_4", A, B, meta, C, s, workspace, thread_k, thread_m, sms, max_par,
           lambda k, n: k * n // 16, torch.int32, lambda k, n: k * n // 16, torch.int16)
+
+
+def mul(A, B, C, s, workspace, thread_k=-1, thread_n=-1, sms=-1, max_par=16):
+    """Dense Marlin FP16 x INT4 multiply: ``C = A @ W``.
+
+    Mirrors ``marlin.mul`` (reference __init__.py:61-75; binding marlin_cuda.cpp:38-64):
+    ``A`` fp16 ``[M, K]``; ``B`` int32 weights in the dense ``Layer.pack`` layout
+    (``K*N/8`` elements); ``C`` fp16 ``[M, N]``, overwritten; ``s`` fp16 scales
+    ``[K/128, N]`` or ``[1, N]``; ``workspace`` int32 with at least ``N/128*max_par``
+    elements (neither read nor written).  Unlike ``mul_2_4`` the binding names the
+    batch ``m`` and the output features ``n``, and the group size is in dense K."""
+    lib = _lib.load()
+    prob_m, prob_n, prob_k = A.size(0), C.size(1), A.size(1)
+    groupsize = -1 if s.size(0) == 1 else prob_k // s.size(0)
+    if groupsize != -1 and groupsize * s.size(0) != prob_k:
+        raise RuntimeError(f"k={prob_k} not compatible with {s.size(0)} groups.")
+    if workspace.numel() < prob_n // 128 * max_par:
+        raise RuntimeError(f"workspace must be of size at least {prob_n // 128 * max_par}.")
+    _check_operands(A, B, None, C, s, workspace, prob_k * prob_n // 8, torch.int32, 0, torch.int16)
+    stream = torch.cuda.current_stream(A.device).cuda_stream
+    err = lib.marlin_hip_mul(_ptr(A), _ptr(B), _ptr(C), _ptr(s), prob_m, prob_n, prob_k, _ptr(workspace),
+                             groupsize, A.get_device(), ctypes.c_void_p(stream), thread_k, thread_n, sms, max_par)
+    if err == _lib.OK:
+        return
+    if err == _lib.ERR_PROB_SHAPE:
+        raise RuntimeError(f"Problem (m={prob_m}, n={prob_n}, k={prob_k}) not compatible with "
+                           f"thread_k={thread_k}, thread_n={thread_n}.")
+    if err == _lib.ERR_KERN_SHAPE:
+        raise RuntimeError(f"No kernel implementation for thread_k={thread_k}, thread_n={thread_n}, "
+                           f"groupsize={groupsize}.")
+    raise RuntimeError(_lib.last_error() or f"marlin_hip error {err}")
 
 
 _KERNELS = {-1: None, 0: "decode", 1: "large_m", 2: "general"}
@@ -580,6 +617,104 @@ class Layer_2_4(nn.Module):
         self.meta = meta.to(self.meta.device)
         if getattr(self, "Bn", None) is not None:  # a native copy of the old weight is stale
             self.to_native()
+
+
+# ---------------------------------------------------------------------------
+# Dense Marlin layout and module (reference __init__.py:78-99, 134-226)
+# ---------------------------------------------------------------------------
+
+
+def _dense_block_index() -> torch.Tensor:
+    """Flat index (16 k x 64 n block, row-major) of nibble t of word w of one dense
+    Marlin block (a 16-deep k-tile of a 64-column chunk): word w = 16 ci + 4 rq + jt
+    holds columns 16 jt + ci (nibbles 0, 1, 4, 5) and 16 jt + ci + 8 (nibbles 2, 3, 6,
+    7) at k = 2 rq + {0, 8, 0, 8, 1, 9, 1, 9}[t].  The same placement as the reference
+    pack's tile permutation (__init__.py:78-99, 214-219), written as a closed form."""
+    w = torch.arange(128)[:, None]
+    t = torch.arange(8)[None, :]
+    jt, rq, ci = w % 4, (w // 4) % 4, w // 16
+    koff = torch.tensor([0, 8, 0, 8, 1, 9, 1, 9])[t]
+    blk = torch.tensor([0, 0, 1, 1, 0, 0, 1, 1])[t]
+    return ((2 * rq + koff) * 64 + 16 * jt + ci + 8 * blk).reshape(-1)
+
+
+def _pack_dense_scales(s: torch.Tensor, n: int, grouped: bool) -> torch.Tensor:
+    """Grouped: within 64 columns slot 8i + j holds column i + 8j (an 8 x 8
+    transpose); per column: within 32 columns slot 8i + t holds column
+    2i + {0, 1, 8, 9, 16, 17, 24, 25}[t] (reference __init__.py:93-98)."""
+    if grouped:
+        return s.reshape(-1, 8, 8).transpose(1, 2).reshape(-1, n).contiguous()
+    return s.reshape(-1, 4, 4, 2).permute(0, 2, 1, 3).reshape(-1, n).contiguous()
+
+
+def pack_dense(w: torch.Tensor, scales: torch.Tensor, groupsize: int = -1):
+    """Pack a K x N fp16 weight into the dense Marlin layout: ``(B [K/16, 2N] int32,
+    s)`` (reference ``Layer.pack(linear, scales)``, __init__.py:177-226): codes
+    ``clamp(round(w / s) + 8, 0, 15)``, eight per int32."""
+    if w.dtype != torch.half:
+        raise ValueError("Only `torch.half` weights are supported.")
+    k, n = w.shape
+    if k % 16 or n % 64:
+        raise ValueError("the dense layout needs K % 16 == 0 and N % 64 == 0")
+    g = k if groupsize == -1 else groupsize
+    q = _quant_codes(w, scales, k, n, g, 15)
+    s = _pack_dense_scales(scales, n, g != k)
+    blocks = q.reshape(k // 16, 16, n // 64, 64).permute(0, 2, 1, 3).reshape(k // 16, n // 64, 1024)
+    codes = blocks[..., _dense_block_index().to(q.device)].reshape(k // 16, n // 64 * 128, 8)
+    return _nibbles_to_int32(codes.reshape(k // 16, -1)), s
+
+
+class Layer(nn.Module):
+    """PyTorch dense Marlin layer; 4-bit (symmetric grouped) linear layer without bias
+    (reference __init__.py:134-226), computed by :func:`mul`.
+
+    Differences from the reference: the out-features check is the intended one
+    (``outfeatures % 256``; the reference's chained comparison checks nothing,
+    __init__.py:145), the workspace follows the module's device, and
+    ``pack(..., trans=True)`` (the transposed permutation, which this kernel does
+    not read) raises.
+    """
+
+    def __init__(self, infeatures, outfeatures, groupsize=-1):
+        super().__init__()
+        if groupsize not in [-1, 128]:
+            raise ValueError("Only groupsize -1 and 128 are supported.")
+        if infeatures % 128 != 0 or outfeatures % 256 != 0:
+            raise ValueError("`infeatures` must be divisible by 128 and `outfeatures` by 256.")
+        if groupsize == -1:
+            groupsize = infeatures
+        if infeatures % groupsize != 0:
+            raise ValueError("`infeatures` must be divisible by `groupsize`.")
+        self.k = infeatures
+        self.n = outfeatures
+        self.groupsize = groupsize
+        self.register_buffer("B", torch.empty((self.k // 16, self.n * 16 // 8), dtype=torch.int))
+        self.register_buffer("s", torch.empty((self.k // groupsize, self.n), dtype=torch.half))
+        self.register_buffer("workspace", torch.zeros(self.n // 128 * 16, dtype=torch.int), persistent=False)
+
+    def forward(self, A):
+        C = torch.empty(A.shape[:-1] + (self.s.shape[1],), dtype=A.dtype, device=A.device)
+        ws = self.workspace
+        if ws.device != A.device:
+            ws = self.workspace = ws.to(A.device)
+        mul(A.view((-1, A.shape[-1])), self.B, C.view((-1, C.shape[-1])), self.s, ws)
+        return C
+
+    def pack(self, linear, scales, trans=False):
+        """Pack a fake-quantized linear layer (``linear.weight`` read as K x N, as the
+        reference does, __init__.py:193) with ``scales`` ``[K/groupsize, N]``."""
+        if linear.weight.dtype != torch.half:
+            raise ValueError("Only `torch.half` weights are supported.")
+        if trans:
+            raise ValueError("trans=True selects the transposed Marlin permutation, which the dense kernel "
+                             "does not read; call pack(linear, scales).")
+        w = linear.weight.data
+        if tuple(w.shape) != (self.k, self.n):
+            raise ValueError(f"weight shape {tuple(w.shape)} != (k, n) = {(self.k, self.n)}")
+        gs = -1 if self.groupsize == self.k else self.groupsize
+        B, s = pack_dense(w, scales.to(w.device), gs)
+        self.B[:, :] = B.to(self.B.device)
+        self.s[:, :] = s.to(self.s.device)
 
 
 def replace_linear(module, name_filter=lambda n: True, groupsize=-1, name=""):

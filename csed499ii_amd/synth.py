@@ -79,3 +79,21 @@ def weight_bytes(K: int, N: int, bits: int = 4, groupsize: int = 128) -> int:
     fp16 scales (K/128)*N*2 (25/64*K*N for 4-bit values and group 128)."""
     g = K if groupsize == -1 else groupsize
     return K * N // 2 * bits // 8 + K * N // 8 + (K // g) * N * 2
+
+
+def make_dense_weight(K: int, N: int, seed: int, groupsize: int = 128, device="cuda", std: float = 0.02):
+    """Packed dense INT4 weight (no pruning) in the dense Marlin layout:
+    ``{"B": int32 [K/16, 2N], "s": fp16, "bits": "dense", ...}``."""
+    from .marlin import pack_dense
+
+    gen = torch.Generator().manual_seed(seed)
+    w = (torch.randn((K, N), generator=gen) * std).to(torch.float16).to(device)
+    _, s, _ = quantize(w, groupsize, 15)
+    B, sp = pack_dense(w, s, groupsize)
+    return {"B": B, "meta": B, "s": sp, "groupsize": groupsize, "bits": "dense", "K": K, "N": N}
+
+
+def dense_weight_bytes(K: int, N: int, groupsize: int = 128) -> int:
+    """Algorithmic bytes of a dense INT4 weight: codes K*N/2 + fp16 scales."""
+    g = K if groupsize == -1 else groupsize
+    return K * N // 2 + (K // g) * N * 2

@@ -86,6 +86,18 @@ int marlin_hip_mul_2_4_noalloc(const void* A, const void* B, const void* meta, v
 int marlin_hip_plan(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, int thread_m, int sms,
                     int noalloc, int* out);
 
+/* Dense INT4 x FP16 GEMM, C[M,N] = A[M,K] * W[K,N], W in the dense Marlin pack()
+ * layout (B int32 [K/16][2N], s fp16 [K/128][N] or [1][N]).  Replaces
+ * marlin::marlin_cuda (kernel_experiments/sparse_marlin/src/marlin/
+ * marlin_cuda_kernel.cu:655-658), same parameter order and meaning: unlike
+ * marlin_hip_mul_2_4, prob_m = M (batch rows), prob_n = N, and groupsize is in dense
+ * K units (128 or -1).  Codes and tile rules as the reference (thread_k, thread_n) =
+ * (128, 128) for M <= 16 or (64, 256); workspace and max_par are accepted for
+ * signature compatibility and not used (split-K scratch as above). */
+int marlin_hip_mul(const void* A, const void* B, void* C, void* s, int prob_m, int prob_n, int prob_k,
+                   void* workspace, int groupsize, int dev, hipStream_t stream, int thread_k, int thread_n,
+                   int sms, int max_par);
+
 /* Same GEMM with 3-bit-compressed metadata (48 uint32 per 64-word group) as
  * produced by marlin_hip_meta3_pack.  Replaces the generated
  * decode_fetch::marlin_cuda_2_4 (kernel_experiments/sparse_marlin/metadata_decode/

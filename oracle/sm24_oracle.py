@@ -611,3 +611,102 @@ def native_dequant(Wn, Xn, Sn, K: int, N: int, groupsize: int) -> np.ndarray:
                             sc = s_nat[k // gs, n]
                             W[n, k] = np.float16(np.float16(code - 8) * sc)
     return W.T.copy()
+
+
+# --------------------------------------------------------------------------
+# Dense Marlin layout (MRL:78-99 ``_get_perms``, MRL:177-226 ``Layer.pack``)
+# --------------------------------------------------------------------------
+
+
+def get_perms_dense():
+    """Restatement of ``_get_perms`` (MRL:78-99), step by step: for each of the 32
+    groups i of 32 entries, the 8 sources (output block b, row pair of i % 4) of
+    column i // 4 in tile 0, repeated for the 4 tiles of a 1024-entry chunk; then the
+    entries of every 8 reordered by [0, 2, 4, 6, 1, 3, 5, 7].  Returns
+    ``(perm[1024], scale_perm[64], scale_perm_single[32])``; ``perm[d]`` is the source
+    index ``256 * tile + 16 * k + n`` (k, n within the 16 x 16 tile) of destination
+    nibble ``d`` (word ``d // 8``, nibble ``d % 8``) of the chunk."""
+    perm = []
+    for i in range(32):
+        rows = (2 * (i % 4), 2 * (i % 4) + 1, 2 * (i % 4) + 8, 2 * (i % 4) + 9)
+        first = [16 * row + i // 4 + 8 * blk for blk in (0, 1) for row in rows]
+        for tile in range(4):
+            perm.extend(x + 256 * tile for x in first)
+    perm = np.asarray(perm, dtype=np.int64).reshape(-1, 8)[:, [0, 2, 4, 6, 1, 3, 5, 7]].ravel()
+    scale_perm = np.asarray([i + 8 * j for i in range(8) for j in range(8)], dtype=np.int64)
+    scale_perm_single = np.asarray([2 * i + j for i in range(4) for j in (0, 1, 8, 9, 16, 17, 24, 25)],
+                                   dtype=np.int64)
+    return perm, scale_perm, scale_perm_single
+
+
+#: Row (within the 16-deep k-tile) and output block of nibble t of a dense word:
+#: low nibbles of bytes 0/2 hold k = 2rq / 2rq+1 and the high nibbles 2rq+8 / 2rq+9
+#: of column ci; bytes 1/3 the same of column ci + 8.
+_DENSE_KOFF = np.array([0, 8, 0, 8, 1, 9, 1, 9], dtype=np.int64)
+_DENSE_BLK = np.array([0, 0, 1, 1, 0, 0, 1, 1], dtype=np.int64)
+
+
+def dense_word_coords(K: int, N: int):
+    """Closed form of the dense layout: for ``B`` of shape ``[K/16, 2N]`` int32 returns
+    ``k, n`` of shape ``[K/16, 2N, 8]``: nibble t of ``B[r, 128 c + w]`` holds the code
+    of ``k = 16 r + 2 rq + KOFF[t]`` and ``n = 64 c + 16 jt + ci + 8 BLK[t]`` with
+    ``jt = w % 4``, ``rq = (w // 4) % 4``, ``ci = w // 16``."""
+    R = K // 16
+    r = np.arange(R)[:, None, None]
+    w = np.arange(2 * N)[None, :, None]
+    t = np.arange(8)[None, None, :]
+    c, wl = w // 128, w % 128
+    jt, rq, ci = wl % 4, (wl // 4) % 4, wl // 16
+    k = 16 * r + 2 * rq + _DENSE_KOFF[t]
+    n = 64 * c + 16 * jt + ci + 8 * _DENSE_BLK[t]
+    return np.broadcast_to(k, (R, 2 * N, 8)), np.broadcast_to(n, (R, 2 * N, 8))
+
+
+def dense_pack(w: np.ndarray, s: np.ndarray, groupsize: int):
+    """Restatement of the dense ``Layer.pack(linear, scales)`` (MRL:177-226, the default
+    ``trans=False`` permutation): codes ``clamp(round(w / s) + 8, 0, 15)`` of the K x N
+    weight (``linear.weight`` read as K x N, MRL:193), placed by ``get_perms_dense``
+    over 16 x 16 tiles (MRL:213-219), 8 nibbles per int32 (MRL:220-223); scales
+    permuted by ``scale_perm`` (grouped) or ``scale_perm_single``.  Returns
+    ``(B[K/16, 2N] int32, s_packed)``."""
+    w = np.asarray(w, dtype=np.float16)
+    K, N = w.shape
+    g = K if groupsize == -1 else groupsize
+    sg = np.asarray(s, dtype=np.float16).reshape(K // g, N)
+    ratio = (w.reshape(K // g, g, N).astype(np.float32) / sg[:, None, :].astype(np.float32)).astype(np.float16)
+    q = np.clip(np.round(ratio.astype(np.float64)).astype(np.int64) + 8, 0, 15).reshape(K, N)
+    perm, scale_perm, scale_perm_single = get_perms_dense()
+    sp = scale_perm if g != K else scale_perm_single
+    s_packed = sg.reshape(-1, sp.size)[:, sp].reshape(K // g, N)
+    tiles = q.reshape(K // 16, 16, N // 16, 16).transpose(0, 2, 1, 3).reshape(K // 16, N * 16)
+    res = tiles.reshape(-1, perm.size)[:, perm].reshape(K // 16, N * 16).astype(np.uint32)
+    words = np.zeros((K // 16, 2 * N), dtype=np.uint32)
+    for t in range(8):
+        words |= res[:, t::8] << np.uint32(4 * t)
+    return words.view(np.int32), s_packed
+
+
+def dense_unpack_codes(B: np.ndarray, K: int, N: int) -> np.ndarray:
+    """Inverse of the dense layout through the closed form: codes ``q[K, N]``."""
+    words = np.ascontiguousarray(B).view(np.uint32).reshape(K // 16, 2 * N)
+    k, n = dense_word_coords(K, N)
+    nib = (words[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 15
+    q = np.zeros((K, N), dtype=np.int64)
+    q[k, n] = nib
+    return q
+
+
+def dense_unpack_scales(s_packed: np.ndarray, K: int, N: int, groupsize: int) -> np.ndarray:
+    g = K if groupsize == -1 else groupsize
+    _, scale_perm, scale_perm_single = get_perms_dense()
+    sp = scale_perm if g != K else scale_perm_single
+    return np.asarray(s_packed, dtype=np.float16).reshape(-1, sp.size)[:, np.argsort(sp)].reshape(K // g, N)
+
+
+def dense_dequant(B, s_packed, K: int, N: int, groupsize: int) -> np.ndarray:
+    """Dense fp16 weight ``W[K, N] = (q - 8) * s`` (fp16 product, as the kernel's
+    dequant and scale, marlin_cuda_kernel.cu:334-349)."""
+    q = dense_unpack_codes(B, K, N)
+    g = K if groupsize == -1 else groupsize
+    srow = np.repeat(dense_unpack_scales(s_packed, K, N, groupsize), g, axis=0)
+    return ((q - 8).astype(np.float16).astype(np.float32) * srow.astype(np.float32)).astype(np.float16)

@@ -135,3 +135,20 @@ def test_probe_library_exports(built_lib):
     out = subprocess.run(["nm", "-D", "--defined-only", str(build.PROBE_LIB)], capture_output=True, text=True,
                          check=True).stdout
     assert declared <= set(re.findall(r"\bT\s+(marlin_probe_\w+)", out))
+
+
+@pytest.mark.parametrize("args,expected", [
+    # dense (prob_m = batch, prob_n = N, prob_k = K, groupsize in dense K, thread_k, thread_n)
+    ((16, 512, 1024, -1, 128, 100), _lib.ERR_PROB_SHAPE),   # N % thread_n
+    ((16, 512, 1000, -1, -1, -1), _lib.ERR_PROB_SHAPE),     # K % 128 (auto tile for batch <= 16)
+    ((32, 384, 1024, 128, -1, -1), _lib.ERR_PROB_SHAPE),    # N % 256 (auto tile above 16 rows)
+    ((32, 512, 1024, -1, 128, 128), _lib.ERR_KERN_SHAPE),   # 128x128 only for one 16-row block
+    ((16, 512, 1024, 64, -1, -1), _lib.ERR_KERN_SHAPE),     # group_blocks 4 not instantiated
+    ((0, 512, 1024, -1, -1, -1), _lib.OK),                  # empty problem
+])
+def test_dense_host_validation_codes(built_lib, args, expected):
+    """marlin_hip_mul refuses shapes with the reference dispatch's codes
+    (marlin_cuda_kernel.cu:660-683, 711-721) before any launch."""
+    m, n, k, g, tk, tn = args
+    null = ctypes.c_void_p(0)
+    assert built_lib.marlin_hip_mul(null, null, null, null, m, n, k, null, g, 0, null, tk, tn, -1, 16) == expected

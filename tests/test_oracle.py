@@ -311,3 +311,73 @@ def test_native_lane_word_positions():
     assert nz.tolist() == [[2, 1, 16 * 2 + 5, 3]]
     assert Wn[2, 1, 37, 3] == 9 << (4 * int(o.NATIVE_NIBBLE[5]))
     assert o.NATIVE_NIBBLE.tolist() == [0, 4, 1, 5, 2, 6, 3, 7]
+
+
+# ---- dense Marlin layout (MRL:78-99, 177-226) ----
+
+
+def test_dense_perm_is_bijection_and_matches_closed_form():
+    """Two derivations of the dense layout agree: the restated construction steps of
+    ``_get_perms`` and the closed form ``dense_word_coords``."""
+    perm, scale_perm, scale_perm_single = o.get_perms_dense()
+    assert sorted(perm.tolist()) == list(range(1024))
+    assert sorted(scale_perm.tolist()) == list(range(64))
+    assert sorted(scale_perm_single.tolist()) == list(range(32))
+    d = np.arange(1024)
+    tile, kk, nn = perm // 256, (perm % 256) // 16, perm % 16
+    k, n = o.dense_word_coords(16, 64)
+    assert np.array_equal(k[0, d // 8, d % 8], kk)
+    assert np.array_equal(n[0, d // 8, d % 8], 16 * tile + nn)
+
+
+@pytest.mark.parametrize("K,N", [(16, 64), (64, 128), (256, 512)])
+def test_dense_word_coords_bijection(K, N):
+    k, n = o.dense_word_coords(K, N)
+    flat = (k * N + n).ravel()
+    assert np.array_equal(np.sort(flat), np.arange(K * N))
+
+
+def test_dense_word_meaning_known_answer():
+    """Word 16 ci + 4 rq + jt of row r: columns 16 jt + ci (byte 0, 2) and + 8 (bytes
+    1, 3); low nibbles k = 2rq (bytes 0, 1) and 2rq + 1 (bytes 2, 3), high nibbles
+    2rq + 8 and 2rq + 9 (the A-fragment rows of the reference's m16n8k16 MMA)."""
+    K, N = 32, 128
+    q = np.zeros((K, N), dtype=np.int64)
+    # plant distinct codes at the eight positions of word (r=1, c=1, ci=5, rq=2, jt=3)
+    r, c, ci, rq, jt = 1, 1, 5, 2, 3
+    planted = {}
+    for t, (dk, db) in enumerate(zip([0, 8, 0, 8, 1, 9, 1, 9], [0, 0, 1, 1, 0, 0, 1, 1])):
+        kk, nn = 16 * r + 2 * rq + dk, 64 * c + 16 * jt + ci + 8 * db
+        q[kk, nn] = t + 3
+        planted[t] = t + 3
+    s = np.ones((1, N), np.float16)
+    W = ((q - 8) * 1.0).astype(np.float16)
+    B, _ = o.dense_pack(W, s, -1)
+    word = B.view(np.uint32).reshape(K // 16, 2 * N)[r, 128 * c + 16 * ci + 4 * rq + jt]
+    for t, code in planted.items():
+        assert (int(word) >> (4 * t)) & 15 == code
+    assert np.array_equal(o.dense_unpack_codes(B, K, N), q)
+
+
+@pytest.mark.parametrize("K,N,g", [(128, 256, 128), (256, 64, -1), (512, 512, 128)])
+def test_dense_pack_round_trip(K, N, g):
+    """unpack(pack(W)) gives W's codes and scales exactly for on-grid weights."""
+    rng = np.random.default_rng(K + N)
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+    q, s, ref = o.quantize(w, g)
+    B, sp = o.dense_pack(ref, s, g)
+    assert np.array_equal(o.dense_unpack_codes(B, K, N), q)
+    assert np.array_equal(o.dense_unpack_scales(sp, K, N, g).view(np.int16), s.view(np.int16))
+    assert np.array_equal(o.dense_dequant(B, sp, K, N, g).view(np.int16), ref.view(np.int16))
+
+
+def test_dense_planted_layout_mistake_is_caught():
+    """A swapped pair of nibble rows in the closed form breaks agreement with the
+    restated permutation (the check above is not vacuous)."""
+    perm, _, _ = o.get_perms_dense()
+    bad = np.array([0, 8, 0, 8, 9, 1, 1, 9])
+    w = np.arange(128)[:, None]
+    t = np.arange(8)[None, :]
+    k_bad = 2 * ((w // 4) % 4) + bad[t]
+    d = np.arange(1024)
+    assert not np.array_equal(k_bad[d // 8, d % 8], (perm % 256) // 16)

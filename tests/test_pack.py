@@ -199,3 +199,40 @@ def test_mul_2_4_binding_checks_on_cpu():
         marlin.mul_2_4(A, B, meta, C, torch.zeros(2, 128, dtype=torch.half), ws[:8])
     with pytest.raises(RuntimeError, match="GPU tensor"):
         marlin.mul_2_4(A, B, meta, C, torch.zeros(2, 128, dtype=torch.half), ws)
+
+
+# ---- dense Marlin packing (reference __init__.py:134-226) ----
+
+
+@pytest.mark.parametrize("K,N,g", [(128, 256, 128), (256, 512, -1), (1024, 768, 128), (512, 256, -1)])
+def test_pack_dense_matches_oracle(K, N, g):
+    """The product's closed-form placement equals the oracle's restated permutation
+    (reference __init__.py:78-99, 213-223), codes and scales bit-exact."""
+    gen = torch.Generator().manual_seed(K + 3 * N)
+    w = (torch.randn((K, N), generator=gen) * 0.02).half()
+    _, s, _ = synth.quantize(w, g)
+    B, sp = marlin.pack_dense(w, s, g)
+    Bo, spo = o.dense_pack(w.numpy(), s.numpy(), g)
+    assert B.shape == (K // 16, 2 * N) and B.dtype == torch.int32
+    assert np.array_equal(B.numpy(), Bo)
+    assert np.array_equal(sp.numpy().view(np.int16), np.asarray(spo, np.float16).view(np.int16))
+
+
+def test_dense_layer_pack_and_checks():
+    K, N = 256, 512
+    gen = torch.Generator().manual_seed(9)
+    w = (torch.randn((K, N), generator=gen) * 0.02).half()
+    _, s, ref = synth.quantize(w, 128)
+    layer = marlin.Layer(K, N, groupsize=128)
+    lin = nn.Linear(K, N)
+    lin.weight.data = ref  # read as K x N, as the reference does
+    layer.pack(lin, s)
+    Bo, spo = o.dense_pack(ref.numpy(), s.numpy(), 128)
+    assert np.array_equal(layer.B.numpy(), Bo)
+    assert set(layer.state_dict()) == {"B", "s"}
+    with pytest.raises(ValueError, match="transposed"):
+        layer.pack(lin, s, trans=True)
+    with pytest.raises(ValueError, match="divisible"):
+        marlin.Layer(K, 320)
+    with pytest.raises(ValueError, match="groupsize"):
+        marlin.Layer(K, N, groupsize=64)
