@@ -6,10 +6,14 @@ fallback: when the library is missing every GPU entry point raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 import threading
 
-LIB_PATH = pathlib.Path(__file__).resolve().with_name("libmarlin_hip.so")
+#: The in-tree build; MARLIN_HIP_LIB names another build of the same library (read
+#: once, at import).
+LIB_PATH = pathlib.Path(os.environ.get("MARLIN_HIP_LIB") or
+                        pathlib.Path(__file__).resolve().with_name("libmarlin_hip.so"))
 
 OK = 0
 ERR_PROB_SHAPE = 1

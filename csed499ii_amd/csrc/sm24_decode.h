@@ -1,26 +1,28 @@
-// Decode-sized (M <= 32) 2:4 INT4 x FP16 GEMM for gfx950, no split-K.
+// Decode-sized (M <= 32) 2:4 INT4 x FP16 GEMM for gfx950.
 //
 // One workgroup owns a tile of TC output columns (TC = 16, 32 or 64) over the whole
-// K, so the result never crosses workgroups: a cross-workgroup hand-off costs
-// microseconds on this multi-XCD part, more than the whole weight stream of a
-// 4096x4096 layer.
+// K, or over one of a.splits contiguous ranges of its stages (split-K: the host sums
+// the ranges through its scratch).  Unsplit, the result never crosses workgroups: a
+// cross-workgroup hand-off costs microseconds on this multi-XCD part, more than the
+// whole weight stream of a 4096x4096 layer.
 //
 // Cost model (measured on MI355X): every 16-byte vector load instruction occupies a
 // compute unit's address path for ~16 cycles whatever its lanes do (full, masked,
 // duplicated or out of range alike), so the kernel issues as few load instructions
 // as the bytes allow and fills every lane with a distinct useful 16-byte piece.
 //
-// A stage covers KS = NW * max(2, 64 / TC) k-blocks of the tile.  Its
-// pieces - packed values, metadata, scales and, for MB < 16, the activation rows -
-// form one list of P 16-byte pieces; thread t loads pieces t, t + NT, ... (SL slots)
-// of every stage, rows clamped to the operand, into a register ring D stages deep.
-// When a stage is due its pieces are written to one of two LDS buffers and, after
-// one barrier, the NW waves read their MFMA operands from LDS.  For MB = 16 (32: two
-// 16-row blocks, each weight fragment feeding two MFMAs) every
-// lane of the activation operand is a real batch row, so each wave loads its own
-// operands straight into the ring instead.  Batch rows past M read row M-1 (their
-// outputs are not stored); k-blocks past K read zero activations, so the last stage
-// needs no per-k-block branch.
+// A stage covers KS = NW * KPW k-blocks of the tile, KPW = max(2, 64 / TC) per wave.
+// Each wave streams its own KPW k-blocks: their pieces - packed values, metadata,
+// the scales of their one scale group and, for MB < 16, the activation rows - form a
+// list of P 16-byte pieces; lane l loads pieces l, l + 64, ... (SL slots) of every
+// stage, rows clamped to the operand, into a register ring D stages deep.  When a
+// stage is due the wave writes its pieces to one of its two LDS buffers and reads its
+// MFMA operands back: a wave's LDS operations complete in order, so no workgroup
+// barrier runs between stages.  For MB = 16 (32: two 16-row blocks, each weight
+// fragment feeding two MFMAs) every lane of the activation operand is a real batch
+// row, so each wave loads its activations straight into the ring instead.  Batch rows
+// past M read row M-1 (their outputs are not stored); k-blocks past K read zero
+// activations, so the last stage needs no per-k-block branch.
 //
 // MFMA (v_smfmac_f32_16x16x64_f16, two k-blocks per instruction) lane roles: lane
 // (rho, h) = (l % 16, l / 16) holds output column n = n0 + 16*cb + rho, i.e. word j =
@@ -56,15 +58,17 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int SPG = TC / 8;                           // 16-byte scale pieces per scale group
   constexpr bool STAGED = MB < 16;                      // activations through LDS
   constexpr int RB = MB > 16 ? MB / 16 : 1;             // 16-row batch blocks (MFMA B operands)
-  constexpr int NB = KS * BPK;
-  constexpr int NM = KS * MPK;
-  constexpr int NSC = GROUPED ? (KS / 4) * SPG : 0;
-  constexpr int NPA = STAGED ? KS * 4 * MB : 0;         // activation pieces (4 per row and k-block)
+  // Pieces of one wave's stage, in its LDS region in this order.
+  constexpr int NB = KPW * BPK;
+  constexpr int NM = KPW * MPK;
+  constexpr int NSC = GROUPED ? SPG : 0;                // KPW <= 4 k-blocks: one scale group
+  constexpr int NPA = STAGED ? KPW * 4 * MB : 0;        // activation pieces (4 per row and k-block)
   constexpr int P1 = NB + NM, P2 = P1 + NSC, P = P2 + NPA;
-  constexpr int SL = (P + NT - 1) / NT;                 // load slots per thread and stage
+  constexpr int SL = (P + 63) / 64;                     // load slots per lane and stage
   constexpr int DA = STAGED ? 0 : KPW * RB;             // direct activation loads per stage
   constexpr int MOFF = NB * 16, SOFF = MOFF + NM * 16, AOFF = SOFF + NSC * 16;
-  constexpr int STAGE = AOFF + NPA * 16;
+  constexpr int STAGE = AOFF + NPA * 16;                // bytes of one wave's stage
+  static_assert(KPW <= 4 && 4 % KPW == 0, "a wave's k-blocks lie in one scale group");
   // Ring depth: at most ~56 loads in flight per wave (vmcnt counts to 63) and a
   // register budget for the ring that keeps the kernel at <= 128 VGPRs (two
   // 8-wave or four 4-wave workgroups per CU).  Even, so that ring slot i always
@@ -78,11 +82,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
 
-  // Two stage buffers; after the last stage the same LDS holds every wave's partial
-  // tile (16 rows x TC columns of fp32, rows padded to TC + 4) for the reduction.
+  // Two stage buffers per wave; after the last stage the same LDS holds every wave's
+  // partial tile (16 rows x TC columns of fp32, rows padded to TC + 4) for the
+  // reduction.
   constexpr int REDP = TC + 4;
   constexpr int REDB = NW * 16 * REDP * 4;
-  constexpr int LDSB = 2 * STAGE > REDB ? 2 * STAGE : REDB;
+  constexpr int LDSB = 2 * NW * STAGE > REDB ? 2 * NW * STAGE : REDB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDSB];
 
   const int tid = threadIdx.x;
@@ -126,21 +131,22 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const uint8_t* sbase[SL];
   uint32_t sstride[SL], srow0[SL], sper[SL], srmax[SL], slds[SL];
   bool szero[SL];  // activation piece: zero past the last k-block
+  const int kw = wave * KPW;  // first k-block of this wave in a stage
 #pragma unroll
   for (int q = 0; q < SL; q++) {
-    const int pc = cmin(tid + q * NT, P - 1);  // surplus lanes repeat the last piece
+    const int pc = cmin(lane + q * 64, P - 1);  // surplus lanes repeat the last piece
     szero[q] = false;
     if (pc < NB) {
-      const int kk = pc / BPK, w = pc % BPK;
+      const int kl = pc / BPK, w = pc % BPK;
       constexpr int bpc = VF == VAL4 ? 8 : 6;  // packed bytes per column and k-block
       sbase[q] = static_cast<const uint8_t*>(a.B) + bpc * (size_t)n0 + 16 * w;
       sstride[q] = bpc * (uint32_t)N;
-      srow0[q] = kk;
+      srow0[q] = kw + kl;
       sper[q] = KS;
       srmax[q] = nkb - 1;
-      slds[q] = kk * BPK * 16 + 16 * w;
+      slds[q] = kl * BPK * 16 + 16 * w;
     } else if (pc < P1) {
-      const int p = pc - NB, kk = p / MPK, w = p % MPK;
+      const int p = pc - NB, kk = p / MPK, w = p % MPK;  // kk: k-block of the wave's share
       const uint8_t* mb = static_cast<const uint8_t*>(a.meta);
       if constexpr (MF == META4) {
         // two parts (units of the column pairs j>>1 = 0, 1), 2*TC bytes each
@@ -161,14 +167,14 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         sstride[q] = 3 * (uint32_t)N;
         slds[q] = MOFF + kk * MPK * 16 + row * 2 * TC + 16 * wp;
       }
-      srow0[q] = kk;
+      srow0[q] = kw + kk;
       sper[q] = KS;
       srmax[q] = nkb - 1;
     } else if (pc < P2) {
-      const int p = pc - P1, gl = p / SPG, w = p % SPG;
+      const int p = pc - P1, gl = p / SPG, w = p % SPG;  // gl = 0: the wave's one group
       sbase[q] = reinterpret_cast<const uint8_t*>(a.s) + 2 * (size_t)n0 + 16 * w;
       sstride[q] = 2 * (uint32_t)N;
-      srow0[q] = gl;
+      srow0[q] = (kw >> 2) + gl;
       sper[q] = KS / 4;
       srmax[q] = ngroups - 1;
       slds[q] = SOFF + gl * 2 * TC + 16 * w;
@@ -177,21 +183,17 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       const int mm = m < M ? m : M - 1;
       sbase[q] = reinterpret_cast<const uint8_t*>(a.A) + 2 * (size_t)mm * K + 16 * u;
       sstride[q] = 64;
-      srow0[q] = kk;
+      srow0[q] = kw + kk;
       sper[q] = KS;
       srmax[q] = nkb - 1;
       slds[q] = AOFF + (kk * MB + m) * 64 + 16 * u;
       szero[q] = true;
     }
   }
-  // Slot q of this wave holds pieces iff q*NT + 64*wave < P (uniform per wave).
-  // Slot 0 is loaded by every wave (a wave without pieces repeats the last one): a
-  // load under a branch leaves the compiler no exact wait count, and with only
-  // conditional loads in flight every stage would wait for all of them.
-  constexpr bool kLastAll = (SL - 1) * NT + 64 * (NW - 1) < P;  // every wave has a piece in slot SL-1
-  auto slot_live = [&](int q) -> bool {
-    return q == 0 || q < SL - 1 || kLastAll || (SL - 1) * NT + 64 * wave < P;
-  };
+  // Every slot of every wave holds pieces (the last one repeats its final piece in
+  // surplus lanes): loads are never under a branch, so the compiler's waits stay
+  // exact.
+  auto slot_live = [&](int) -> bool { return true; };
   // Activation pieces past the last k-block read the zero buffer (an address select:
   // a select on the loaded value would wait for the load right away).
   const uint8_t* zeros = reinterpret_cast<const uint8_t*>(a.zeros);
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     const uint32_t row = (uint32_t)(st0 + s) * sper[q] + srow0[q];
     const uint32_t r = row < srmax[q] ? row : srmax[q];
     const uint8_t* p = sbase[q] + (uint64_t)r * sstride[q];
-    if (q * NT + NT > P2) {  // the slot may hold activation pieces
+    if (q * 64 + 64 > P2) {  // the slot may hold activation pieces
       if (szero[q] && row > srmax[q]) p = zeros;
     }
     return *reinterpret_cast<const u32x4*>(p);
@@ -227,13 +229,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 
   // Per-lane LDS byte offsets of this wave's first k-block and column block; the
   // k-block pair (q2), column block (cb) and buffer parts are immediates.
-  const int kw = wave * KPW;                          // first k-block of this wave in a stage
-  const uint32_t o_val = (kw + kh) * (BPK * 16) + (VF == VAL4 ? 4 * (16 * gl + 4 * t0 + j) : 0);
+  // (offsets within the wave's own stage region)
+  const uint32_t o_val = kh * (BPK * 16) + (VF == VAL4 ? 4 * (16 * gl + 4 * t0 + j) : 0);
   const int wi_lane = 16 * gl + 4 * t0 + j;           // 3-bit values: word index without cb
-  const uint32_t o_meta = MOFF + (kw + kh) * (MPK * 16) + jb * 2 * TC + 8 * (2 * gl + jj);
-  const uint32_t o_mrow = MOFF + (kw + kh) * (MPK * 16);
-  const uint32_t o_scale = SOFF + (kw >> 2) * 2 * TC + 2 * (8 * gl + 2 * j + blk);  // same group for the wave
-  const uint32_t o_act = AOFF + (kw * MB + arow) * 64 + 16 * au;
+  const uint32_t o_meta = MOFF + kh * (MPK * 16) + jb * 2 * TC + 8 * (2 * gl + jj);
+  const uint32_t o_mrow = MOFF + kh * (MPK * 16);
+  const uint32_t o_scale = SOFF + 2 * (8 * gl + 2 * j + blk);
+  const uint32_t o_act = AOFF + arow * 64 + 16 * au;
   // Dequant constants held in VGPRs, so that mask-and-or is one v_and_or_b32.
   uint32_t kMask, kMaskHi, kMagic;
   asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
@@ -386,8 +388,9 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     for (int q = 0; q < DA; q++) dring[i][q] = load_direct(i, q);
     __builtin_amdgcn_sched_barrier(0);
   }
+  uint8_t* const wlds = lds + wave * 2 * STAGE;  // this wave's two stage buffers
   auto stage = [&](int i, bool reload, int s) {
-    uint8_t* st = lds + (i & 1) * STAGE;
+    uint8_t* st = wlds + (i & 1) * STAGE;
 #pragma unroll
     for (int q = 0; q < SL; q++) {
       if (slot_live(q)) {
@@ -395,7 +398,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         if (reload) ring[i][q] = load_slot(q, s + D);
       }
     }
-    __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     compute(st, dring[i]);
     if (reload) {

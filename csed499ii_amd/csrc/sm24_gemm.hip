@@ -544,16 +544,20 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 
 // Column-tile width, waves per workgroup and K splits of the decode kernel, from
 // measured single-call times on MI355X (Llama-2-7B and -70B shapes, M in {1, 2, 4, 8,
-// 16, 24, 32}, every forced choice).  Narrow N (fewer than CUs/2 64-column chunks) takes
+// 16, 24, 32}, every forced choice of TC in {16, 32, 64}, NW in {4, 8} and splits in
+// {1, 2, 4}, on one box).  Narrow N (fewer than CUs/2 64-column chunks) takes
 // 16-column tiles for enough workgroups, until M grows: every tile re-reads all M
-// activation rows over K, so from M = 8 (long K) or M > 16 wider tiles split along K
-// keep the workgroup count while cutting that traffic (down 11008x4096 at M = 32:
-// 23.4 -> 13.5 us).  Wider N takes 64-column tiles from M = 8, below that 32-column
-// tiles when N/32 is at least twice the CU count, else 16; from M = 8 its 64-column
-// tiles split K in two.  A split costs a hand-off through the uncached scratch
-// (>= 2.5 us), so it is used only where measured to pay.  Long K (>= 8192) at wider
-// N splits K four ways at N <= 10240 (Llama-2-70B qkv, o, down: 707 -> 589 us over
-// M in {1..32}, within 1.4 % of the best forced choice per call).
+// activation rows over K, so from M = 5 (long K) or M > 16 64-column tiles split
+// four ways along K keep the workgroup count while cutting that traffic (down
+// 11008x4096 at M = 8: 9.13 -> 8.84 us; o 4096x4096 at M = 32: 8.46 -> 7.83 us).
+// Wider N takes 64-column tiles from M = 8, below that 32-column tiles when N/32 is at
+// least twice the CU count, else 16.  A split costs a hand-off through the uncached
+// scratch (>= 2.5 us), so it is used only where measured to pay.  Long K (>= 8192)
+// at wider N splits K four ways at N <= 10240 (Llama-2-70B qkv, down) and two ways
+// for the widest N from M = 2; Llama-2-70B o (N/16 = 2 per CU) keeps 32-column tiles
+// unsplit up to M = 8 (8.55 -> 7.47 us at M = 1).  7B sweep (M in {1, 2, 4, 8, 16}):
+// 162.4 us summed over the 20 calls, against 168.0 us for the previous kernel, whose
+// LDS stages were shared by the workgroup behind a barrier, on its own table.
 // MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
 struct DecodeShape {
   int tc, nw, splits;
@@ -569,25 +573,23 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   const bool narrow = 2 * (N / 64) < cus;
   const bool longk = K >= 8192;
   if (narrow) {
-    if (longk && M > 16) d = {64, 4, 4};
-    else if (longk && M > 8) d = {64, 8, 4};
-    else if (longk && M > 4) d = {32, 8, 2};
-    else if (M > 16) d = {32, 4, 2};
+    if (M > 16) d = {64, 4, 4};
+    else if (longk && M > 4) d = {64, 8, 4};
     else d = {16, M <= 4 ? 8 : 4, 1};
   } else if (longk) {
-    // long K at wide N (the Llama-2-70B shapes): K splits of 64-column tiles; 16- or
-    // 32-column tiles for few rows where N/16 fills one round of two per CU.
-    if (wide32) d = {64, 4, M > 8 ? 2 : 1};
+    // long K at wide N (the Llama-2-70B shapes): K splits of 64-column tiles; 32-column
+    // tiles for few rows where N/16 fills one round of two per CU.
+    if (wide32) d = M == 1 ? DecodeShape{32, 4, 1} : DecodeShape{64, 4, 2};
     else if (M > 8) d = {64, 4, 4};
     else if (K >= 16384) d = {64, 8, 4};
-    else if (N / 16 <= 2 * cus) d = {M <= 4 ? 16 : 32, 8, 1};
+    else if (N / 16 <= 2 * cus) d = {32, 8, 1};
     else d = {M <= 4 ? 32 : 64, 4, 4};
   } else if (M > 16) {
     d = {64, 4, N / 64 >= cus ? 2 : 1};
   } else if (M >= 8) {
-    d = {64, wide32 ? 4 : 8, N / 64 >= cus ? 2 : 1};
+    d = {64, wide32 ? 4 : 8, 1};
   } else if (wide32) {
-    d = {32, M == 1 ? 4 : 8, 1};
+    d = {32, 4, 1};
   } else {
     d = {16, 4, 1};
   }

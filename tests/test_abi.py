@@ -95,9 +95,10 @@ def test_plan_without_gpu(built_lib):
     p = marlin.plan_2_4(1, 4096, 4096)
     assert p["kernel"] == "decode" and p["splits"] == 1 and p["launches"] == 1
     assert p["workgroups"] * (p["threads"] // 64) > 0
-    p = marlin.plan_2_4(16, 4096, 22016)  # wide N from 8 rows: 64-column tiles split in two
+    assert marlin.plan_2_4(16, 4096, 22016)["splits"] == 1
+    p = marlin.plan_2_4(24, 4096, 22016)  # wide N above 16 rows: 64-column tiles split in two
     assert p["kernel"] == "decode" and p["splits"] == 2 and p["workgroups"] == 22016 // 64 * 2
-    assert marlin.plan_2_4(16, 4096, 22016, noalloc=True)["splits"] == 1
+    assert marlin.plan_2_4(24, 4096, 22016, noalloc=True)["splits"] == 1
     assert marlin.plan_2_4(4, 8192, 8192)["splits"] == 1  # 16-column tiles fill the CUs
     assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4  # long K, wider N: K split four ways
     p = marlin.plan_2_4(64, 4096, 4096)  # below the large-M threshold: two decode launches

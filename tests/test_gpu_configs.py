@@ -53,14 +53,14 @@ def test_prefill_llama70b_full_size(name, M):
 
 def test_two_streams_split_k_overlap():
     """Two layers on two same-priority streams, both planned with split-K (gate_up
-    4096x22016 at M = 16 splits in two, Llama-2-70B qkv 8192x10240 at M = 4 in four),
+    4096x22016 at M = 24 splits in two, Llama-2-70B qkv 8192x10240 at M = 4 in four),
     issued back to back with no synchronisation between them: each stream has its
     own scratch, so both results match the oracle and the sequential results."""
-    assert marlin.plan_2_4(16, 4096, 22016)["splits"] == 2
+    assert marlin.plan_2_4(24, 4096, 22016)["splits"] == 2
     assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4
     w1 = synth.make_weight(4096, 22016, 501, 128, device=DEV)
     w2 = synth.make_weight(8192, 10240, 502, 128, device=DEV)
-    A1 = synth.make_activation(16, 4096, 503, device=DEV)
+    A1 = synth.make_activation(24, 4096, 503, device=DEV)
     A2 = synth.make_activation(4, 8192, 504, device=DEV)
     ref1, ref2 = _mul(A1, w1), _mul(A2, w2)
     torch.cuda.synchronize()
@@ -81,7 +81,7 @@ def test_two_streams_split_k_overlap():
         assert torch.equal(C1, ref1), "gate_up on stream 1 differs from the sequential result"
         assert torch.equal(C2, ref2), "70B o on stream 2 differs from the sequential result"
     t1, t2 = to_cpu(w1), to_cpu(w2)
-    check_slices(C1, A1.cpu().numpy(), t1, (0, 170, 340), 4, "stream 1 gate_up M=16")
+    check_slices(C1, A1.cpu().numpy(), t1, (0, 170, 340), 4, "stream 1 gate_up M=24")
     check_slices(C2, A2.cpu().numpy(), t2, (0, 78, 156), 4, "stream 2 qkv M=4")
 
 

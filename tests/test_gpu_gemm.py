@@ -145,8 +145,9 @@ def _weight70(K, N):
 @pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
 @pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (28672, 8192), (8192, 57344)])
 def test_decode_llama70b_full_size_slices(K, N, M):
-    """The Llama-2-70B decode shapes (long K: 16-, 32- and 64-column tiles, K split
-    four ways), checked on column slices; repeated calls must be bit-identical."""
+    """The Llama-2-70B decode shapes (long K: 32- and 64-column tiles, K unsplit or
+    split two or four ways), checked on column slices; repeated calls must be
+    bit-identical."""
     wt, t = _weight70(K, N)
     A = synth.make_activation(M, K, 70 + M, device=DEV)
     C = _run(wt, A)
