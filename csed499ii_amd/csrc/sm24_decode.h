@@ -45,7 +45,7 @@ namespace sm24 {
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
+template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP, bool RES>
 __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int NT = 64 * NW;                           // threads
   constexpr int NCB = TC / 16;                          // 16-column MFMA blocks per tile
@@ -56,7 +56,11 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // of the 3-bit code words (the whole 192-byte group when TC == 64).
   constexpr int MPK = (MF == META3 && TC == 64) ? 12 : TC / 4;
   constexpr int SPG = TC / 8;                           // 16-byte scale pieces per scale group
-  constexpr bool STAGED = MB < 16;                      // activations through LDS
+  // MB < 16: activations through LDS, either resident (RES: the workgroup's rows over
+  // its whole k range, loaded once by LDS-DMA into the dynamic LDS) or with every
+  // stage's pieces.  MB >= 16: loaded by each wave straight into its MFMA operands.
+  static_assert(!RES || MB < 16, "resident activations are for MB < 16");
+  constexpr bool STAGED = MB < 16 && !RES;              // activations with the stage pieces
   constexpr int RB = MB > 16 ? MB / 16 : 1;             // 16-row batch blocks (MFMA B operands)
   // Pieces of one wave's stage, in its LDS region in this order.
   constexpr int NB = KPW * BPK;
@@ -65,7 +69,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int NPA = STAGED ? KPW * 4 * MB : 0;        // activation pieces (4 per row and k-block)
   constexpr int P1 = NB + NM, P2 = P1 + NSC, P = P2 + NPA;
   constexpr int SL = (P + 63) / 64;                     // load slots per lane and stage
-  constexpr int DA = STAGED ? 0 : KPW * RB;             // direct activation loads per stage
+  constexpr int DA = MB >= 16 ? KPW * RB : 0;          // direct activation loads per stage
   constexpr int MOFF = NB * 16, SOFF = MOFF + NM * 16, AOFF = SOFF + NSC * 16;
   constexpr int STAGE = AOFF + NPA * 16;                // bytes of one wave's stage
   static_assert(KPW <= 4 && 4 % KPW == 0, "a wave's k-blocks lie in one scale group");
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int LPS = SL + DA;
   // DEEP: a ring as deep as the budget allows (long K: more bytes in flight per
   // workgroup); otherwise 16 VGPRs, so that more workgroups are resident per CU.
-  constexpr int RING_VGPRS = !DEEP ? 16 : (STAGED ? 40 : (RB > 1 || TC == 64 ? 48 : 64));
+  constexpr int RING_VGPRS = !DEEP ? 16 : (MB < 16 ? 40 : (RB > 1 || TC == 64 ? 48 : 64));
   constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
@@ -126,6 +130,34 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int n0 = tile * TC;
   const int chunk = n0 >> 6;
   const int g0 = (n0 & 63) >> 3;
+
+  // ---- resident activations (RES): batch rows 0..M-1 of this split's k range, zero
+  // past K, row m at byte m * RS of the dynamic LDS (RS = the range's bytes + 16, so
+  // that the rows start on different banks); every wave copies every NW-th 1 KiB
+  // chunk of each row by LDS-DMA, ahead of the weight ring's first loads ----
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  const uint32_t span = (uint32_t)nst * (KS * 64);  // bytes of one row's k range
+  const uint32_t RS = span + 16;
+  if constexpr (RES) {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    const uint32_t act0 = (uint32_t)(size_t)(lds_u8*)dyn_lds;
+    const int cpr = (int)((span + 1023) >> 10);
+    const int k0 = st0 * KS * 32;
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+      if (m < M) {  // uniform
+        for (int jc = wave; jc < cpr; jc += NW) {
+          const uint32_t b = (uint32_t)jc * 1024u + 16u * lane;
+          if (b < span) {
+            const int k = k0 + (int)(b >> 1);
+            const _Float16* src = k < K ? a.A + (size_t)m * K + k : a.zeros;
+            dma16(act0 + m * RS + (uint32_t)jc * 1024u, src);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // ---- per-slot piece state: bytes at base + min(s*per + row0, rmax) * stride ----
   const uint8_t* sbase[SL];
@@ -263,16 +295,26 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   half8_t sact[KPW];  // staged activation operands (lanes rho >= MB never reload)
 #pragma unroll
   for (int q = 0; q < KPW; q++) sact[q] = (half8_t){};
+  // resident row of the lane (rho < M), at the wave's first k-block of stage 0
+  const uint32_t o_ract = (uint32_t)arow * RS + (uint32_t)kw * 64u + 16u * au;
 
-  auto compute = [&](const uint8_t* st, const half8_t* dact) {
+  // st: the wave's stage buffer; dact: direct activation operands; aoff: byte offset
+  // of the stage in the resident rows
+  auto compute = [&](const uint8_t* st, const half8_t* dact, uint32_t aoff) {
 #pragma unroll
     for (int q2 = 0; q2 < KP; q2++) {
       half16_t act[RB];
-      if constexpr (STAGED) {
+      if constexpr (MB < 16) {
         // Only lanes of real batch rows read the staged row; the other lanes' MFMA
         // columns are never stored, so their operand keeps whatever the register
         // held (LDS reads are paid per active lane).
-        if (rho < MB) {
+        if constexpr (RES) {
+          if (rho < M) {
+            const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
+            sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
+            sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(ap + 64);
+          }
+        } else if (rho < MB) {
           sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
           sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
         }
@@ -388,6 +430,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     for (int q = 0; q < DA; q++) dring[i][q] = load_direct(i, q);
     __builtin_amdgcn_sched_barrier(0);
   }
+  if constexpr (RES) {
+    // every wave's activation DMAs have landed: issued before the D * LPS ring loads,
+    // they are older than every load still allowed in flight
+    wait_vm<D * LPS>();
+    __syncthreads();
+  }
   uint8_t* const wlds = lds + wave * 2 * STAGE;  // this wave's two stage buffers
   auto stage = [&](int i, bool reload, int s) {
     uint8_t* st = wlds + (i & 1) * STAGE;
@@ -399,7 +447,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    compute(st, dring[i]);
+    compute(st, dring[i], (uint32_t)s * (KS * 64));
     if (reload) {
 #pragma unroll
       for (int q = 0; q < DA; q++) dring[i][q] = load_direct(s + D, q);
@@ -448,11 +496,14 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
     __syncthreads();  // the last stage's (or the previous block's) LDS reads are done
+    // only the rows of real batch rows are stored, summed and written
+    if (rho + 16 * rb < M) {
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++)
-      *reinterpret_cast<float4_t*>(red + (wave * 16 + rho) * REDP + 16 * cb + 4 * h) = acc[0][cb][rb];
+      for (int cb = 0; cb < NCB; cb++)
+        *reinterpret_cast<float4_t*>(red + (wave * 16 + rho) * REDP + 16 * cb + 4 * h) = acc[0][cb][rb];
+    }
     __syncthreads();
-    if (tid < 4 * TC) {
+    if (tid < 4 * TC && r_out + 16 * rb < M) {
       float4_t v = *reinterpret_cast<const float4_t*>(red + r_out * REDP + c_out);
 #pragma unroll
       for (int w = 1; w < NW; w++) v += *reinterpret_cast<const float4_t*>(red + (w * 16 + r_out) * REDP + c_out);
@@ -474,7 +525,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     __syncthreads();
     if (arrived != (uint32_t)S) return;
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < 4 * TC) {
+    if (tid < 4 * TC && r_out < M) {
       // up to four splits' partials per batch of loads (the uncached reads are
       // latency-bound: one wait per batch, not per split)
       float4_t v[RB];

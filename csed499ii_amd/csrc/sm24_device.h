@@ -174,6 +174,16 @@ __device__ __forceinline__ void dma_chunk_nos(uint32_t lds, uint32_t vw, const v
       : "memory", "m0");
 }
 
+// One DMA of 16 bytes per lane from the lane's own 64-bit address src into
+// lds + 16 lane (lanes outside the exec mask copy nothing).
+__device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off" ::"s"(lds),
+      "v"(src)
+      : "memory", "m0");
+}
+
 // Waits until at most N vector-memory operations of this wave are in flight.
 template <int N>
 __device__ __forceinline__ void wait_vm() {

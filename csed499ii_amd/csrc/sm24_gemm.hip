@@ -605,12 +605,14 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   return d;
 }
 
-// Register ring depth: deep for long K per split (one workgroup per CU streams more
-// stages at once), shallow for K <= 8192 (more resident workgroups); measured on
-// the Llama-2-7B shapes (K = 4096 and 11008).  MARLIN_HIP_DECODE_DEEP overrides.
+// Register ring depth: shallow (16 VGPRs: more resident workgroups) up to 16384 k per
+// split, measured equal or faster at every Llama-2-7B and -70B decode call of the
+// planner (K per split up to 11008: 7B down at M <= 4 runs 0.55-0.8 us faster than
+// deep); deep (more stages in flight per wave) beyond.  MARLIN_HIP_DECODE_DEEP
+// overrides.
 bool decode_deep(int K, int splits) {
   static const int forced_deep = env_choice("MARLIN_HIP_DECODE_DEEP", {0, 1}, -1);
-  return forced_deep >= 0 ? forced_deep == 1 : K / splits > 8192;
+  return forced_deep >= 0 ? forced_deep == 1 : K / splits > 16384;
 }
 
 // The same decode shape without a K split (no split-K scratch available or wanted).
@@ -623,18 +625,51 @@ void decode_unsplit(DecodeShape& d, int K) {
 // (loaded straight into the MFMA operands: one or two 16-row blocks).
 int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
 
+// Static LDS bytes of a kernel (cached per instantiation by the caller).
+size_t static_lds(const void* fn) {
+  hipFuncAttributes attr{};
+  return hipFuncGetAttributes(&attr, fn) == hipSuccess ? attr.sharedSizeBytes : SIZE_MAX;
+}
+
+// Batches of up to 4 rows keep their activation rows resident in LDS (one copy per
+// workgroup, loaded once: every stage's loads are weight pieces only) when a
+// workgroup runs at least 8 stages and the rows of its k range fit beside the
+// kernel's static LDS in 64 KiB; otherwise each stage carries its activation pieces.
+// Measured on the Llama-2-7B shapes at M in {1, 2, 4}: 0.03-0.47 us faster per call
+// from 8 stages up (gate_up at M = 2: 10.09 -> 9.62 us), 0.07-0.23 us slower for o
+// 4096x4096 (4 stages of 32 k-blocks: the copy and its barrier are not amortised).
+// MARLIN_HIP_DECODE_RES=0 turns it off.
+constexpr size_t kDecodeLdsMax = 64 * 1024;
+template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
+void launch_decode_v(const GemmArgs& a, hipStream_t stream) {
+  static const int forced_res = env_choice("MARLIN_HIP_DECODE_RES", {0, 1}, 1);
+  const dim3 grid(a.N / TC * a.splits), block(64 * NW);
+  if constexpr (MB < 16) {
+    constexpr int ks = NW * (64 / TC > 2 ? 64 / TC : 2);
+    const int nst_all = (a.K / 32 + ks - 1) / ks;
+    const int nst_max = (nst_all + a.splits - 1) / a.splits;
+    const size_t dyn = (size_t)MB * ((size_t)nst_max * ks * 64 + 16);
+    static const size_t stat =
+        static_lds(reinterpret_cast<const void*>(&sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>));
+    if (forced_res == 1 && nst_max >= 8 && stat <= kDecodeLdsMax && dyn <= kDecodeLdsMax - stat) {
+      hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>), grid, block, dyn, stream, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream, a);
+}
+
 template <int TC, int NW, int MB, bool GROUPED>
 void launch_decode_mb(const GemmArgs& a, bool deep, int vf, int mf, hipStream_t stream) {
-  const dim3 grid(a.N / TC * a.splits), block(64 * NW);
   if (vf == VAL3) {
-    if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL3, META4, false>), grid, block, 0, stream, a);
+    if (deep) launch_decode_v<TC, NW, MB, GROUPED, VAL3, META4, true>(a, stream);
+    else launch_decode_v<TC, NW, MB, GROUPED, VAL3, META4, false>(a, stream);
   } else if (mf == META3) {
-    if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META3, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META3, false>), grid, block, 0, stream, a);
+    if (deep) launch_decode_v<TC, NW, MB, GROUPED, VAL4, META3, true>(a, stream);
+    else launch_decode_v<TC, NW, MB, GROUPED, VAL4, META3, false>(a, stream);
   } else {
-    if (deep) hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META4, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VAL4, META4, false>), grid, block, 0, stream, a);
+    if (deep) launch_decode_v<TC, NW, MB, GROUPED, VAL4, META4, true>(a, stream);
+    else launch_decode_v<TC, NW, MB, GROUPED, VAL4, META4, false>(a, stream);
   }
 }
 
