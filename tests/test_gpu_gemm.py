@@ -206,15 +206,25 @@ def test_deterministic_repeats():
         assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
-def test_graph_replay_matches_eager():
-    wt, A = _problem(8, 4096, 4096, 128, 9)
-    ws = torch.zeros(4096 // 128 * 16, dtype=torch.int32, device=DEV)
-    C_eager = torch.empty(8, 4096, dtype=torch.half, device=DEV)
-    marlin.mul_2_4(A, wt["B"], wt["meta"], C_eager, wt["s"], ws)
+@pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (24, 4096, 22016)])
+def test_graph_replay_matches_eager(M, K, N):
+    """Captured calls replay the eager result bit for bit: 8 rows on 4096x4096 (one
+    16-column tile per workgroup, unsplit) and 24 rows on 4096x22016 (K split in two
+    through the capture stream's scratch, which the eager call on that stream made
+    first)."""
+    if M == 24:
+        assert marlin.plan_2_4(M, K, N)["splits"] == 2
+    wt, A = _problem(M, N, K, 128, 9)
+    ws = torch.zeros(N // 128 * 16, dtype=torch.int32, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        C_eager = torch.empty(M, N, dtype=torch.half, device=DEV)
+        marlin.mul_2_4(A, wt["B"], wt["meta"], C_eager, wt["s"], ws)
     torch.cuda.synchronize()
-    C = torch.zeros(8, 4096, dtype=torch.half, device=DEV)
+    C = torch.zeros(M, N, dtype=torch.half, device=DEV)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for _ in range(3):
             marlin.mul_2_4(A, wt["B"], wt["meta"], C, wt["s"], ws)
     for _ in range(4):

@@ -58,10 +58,12 @@ def test_native_gemm_full_oracle(M, K, N, g):
 @pytest.mark.parametrize("M", [1, 4, 8, 16])
 @pytest.mark.parametrize("K,N", [(4096, 12288), (11008, 4096), (8192, 8192), (28672, 8192)])
 def test_native_gemm_full_size_slices(K, N, M):
-    """Llama-2-7B/70B decode shapes: K split when a split's activation rows would
-    exceed 64 KiB of LDS (M = 4 at K = 11008 and 28672, M = 1 never here); checked on
-    column slices against the oracle and whole against mul_2_4 on the original
-    weight; repeated calls bit-identical (split-K hand-off in split order)."""
+    """Llama-2-7B/70B decode shapes.  The native planner splits K in two at M = 4 from
+    K = 16384 (28672x8192), and at 8-16 rows when the widest tile's workgroups cover
+    less than 60 % of the CUs (11008x4096 and 28672x8192 at M = 8, 16); M = 1 never
+    splits.  Checked on column slices against the oracle and whole against mul_2_4
+    on the original weight; repeated calls bit-identical (split-K hand-off in split
+    order)."""
     wt = synth.make_weight(K, N, K + N + M, 128, device=DEV)
     A = synth.make_activation(M, K, 3 + M, device=DEV)
     nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
@@ -95,18 +97,24 @@ def test_native_rejects_bad_shapes():
         _native_run(synth.make_activation(17, 256, 6, device=DEV), nat, 64)
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (4, 11008, 4096), (16, 4096, 4096)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (16, 11008, 4096), (4, 28672, 8192)])
 def test_native_graph_replay_matches_eager(M, K, N):
-    """Captured native calls (one split, and K split through the scratch, grown by
-    the eager call first) replay the eager result bit for bit, with eager work and
-    synchronisations between the replays."""
+    """Captured native calls replay the eager result bit for bit, with eager work and
+    synchronisations between the replays: one unsplit shape and two that split K
+    (11008x4096 at M = 16 four ways, 28672x8192 at M = 4 in two).  The eager call
+    runs first on the capture stream, so that stream already has its split-K
+    scratch and the captured calls split as the eager one did."""
     wt = synth.make_weight(K, N, 77 + M, 128, device=DEV)
     A = synth.make_activation(M, K, 78, device=DEV)
     nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
-    C_eager = _native_run(A, nat, N)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        C_eager = _native_run(A, nat, N)
     C = torch.zeros(M, N, dtype=torch.half, device=DEV)
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         for _ in range(3):
             marlin.mul_2_4_native(A, *nat[:2], C, nat[2])
     for _ in range(4):
@@ -115,6 +123,27 @@ def test_native_graph_replay_matches_eager(M, K, N):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(C, C_eager)
+
+
+@pytest.mark.parametrize("M", [8, 16])
+def test_native_gemm_two_block_tiles(M):
+    """K = 4096, N = 8192 at 8 and 16 rows: the native planner's two-block tiles (four
+    blocks leave too few workgroups, 128 on 256 CUs, and K = 4096 is too short to
+    split), against the oracle on column slices and against mul_2_4 whole."""
+    K, N = 4096, 8192
+    wt = synth.make_weight(K, N, 41 + M, 128, device=DEV)
+    A = synth.make_activation(M, K, 42 + M, device=DEV)
+    nat = marlin.pack_native(wt["B"], wt["meta"], wt["s"])
+    C = _native_run(A, nat, N)
+    assert torch.equal(_native_run(A, nat, N), C), "repeated calls differ"
+    C_ref = torch.empty_like(C)
+    marlin.mul_2_4(A, wt["B"], wt["meta"], C_ref, wt["s"], torch.zeros(N // 128 * 16, dtype=torch.int32, device=DEV))
+    torch.cuda.synchronize()
+    assert_close(C.cpu().numpy(), C_ref.cpu().numpy(), f"native vs mul_2_4 {K}x{N} M={M}")
+    t = to_cpu(wt)
+    for c0 in (0, 62, 124):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"native {K}x{N} M={M} slice {c0}")
 
 
 def test_layer_to_native():
