@@ -595,6 +595,7 @@ def build_workload(args, device):
         class Copy:
             name, K, N, M = "copy", 0, 0, 0
             wbytes = 2 * n  # bytes read (and as many written)
+            kb_bytes = 4 * n  # read + written
             flops = 0
 
             def __call__(self):
