@@ -16,6 +16,7 @@ Reference files restated here (paths relative to the reference checkout):
 * ``kernel_experiments/sparse_marlin/metadata_decode/codec.cu`` (``CODEC``)
 * ``kernel_experiments/sparse_marlin/decoder_dependency/pair.cu`` (``PAIR``)
 * ``kernel_experiments/3bit_encoding/experiment.cu`` (``EXP3``)
+* ``kernel_experiments/sparse_marlin/src/marlin/__init__.py`` dense part (``MRL:61-239``)
 
 How each function is pinned (checks live in ``tests/test_oracle.py``):
 
@@ -50,6 +51,13 @@ native_pack / native_unpack this build's own layout (no reference counterpart):
                             exact round trip with the reference layout; the
                             native fields read by native_dequant (stated without
                             the reference layout) give dequant()'s weight
+get_perms_dense             the dense layout's closed form ``dense_word_coords``
+                            (two derivations agree; a planted swap of nibble rows
+                            is caught); bijections
+dense_word_coords           agrees with get_perms_dense; known answer: codes planted
+                            at the eight positions of one word are read back
+dense_pack / dense_unpack_* round trip unpack(pack(W)) == W's codes and scales,
+dense_dequant               bit-exact, grouped and per-column
 ==========================  ==========================================================
 """
 from __future__ import annotations
