@@ -133,7 +133,8 @@ def kernel_of(c) -> str:
     if getattr(c, "native", False):
         return "sm24::sm24_native_decode_kernel"
     if getattr(c, "bits", None) == "dense":
-        return "sm24::marlin_dense_kernel"
+        big = c.M >= 65 and c.N % 512 == 0 and c.K % 128 == 0
+        return "sm24::marlin_dense_prefill_kernel" if big else "sm24::marlin_dense_kernel"
     min_m = 65 if c.N >= 16384 else (97 if c.N >= 4096 else 160)
     if c.M > 32 and c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
         return "sm24::sm24_prefill_kernel"

@@ -30,7 +30,9 @@
 // 655-736) and marlin_cuda.cpp:38-64 (the binding's checks).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
+#include "marlin_dense_prefill.h"
 #include "sm24_device.h"
 #include "sm24_host.h"
 #include "../../include/marlin_hip.h"
@@ -280,6 +282,69 @@ int dense_splits(int chunks, int ztiles, int nks, int cus) {
   return s;
 }
 
+// Large-M path (marlin_dense_prefill_kernel): N a multiple of its 512-column tile, K of
+// 128 (whole scale groups, an even number of 64-deep k-steps) and 32-bit operand
+// offsets, from MARLIN_HIP_DENSE_PREFILL_MIN_M rows (default 65).
+bool dense_prefill_fits(int M, int N, int K) {
+  static const int forced_min_m = [] {
+    const char* e = getenv("MARLIN_HIP_DENSE_PREFILL_MIN_M");
+    const int x = e ? atoi(e) : 0;
+    return x >= 1 ? x : 0;
+  }();
+  const int min_m = forced_min_m ? forced_min_m : 65;
+  return M >= min_m && N % kDpTileCols == 0 && K % 128 == 0 && (long long)M * K < (1LL << 31) - 2048 &&
+         (long long)K * N < (1LL << 33);
+}
+
+// K splits of the dense large-M kernel, by the 2:4 prefill planner's model: rounds of
+// one workgroup per CU times the k-steps per split, plus the partial exchange (each
+// split stores a 256 KiB fp32 tile), at ~1.3 us per 64-deep k-step of a tile (32
+// MFMAs per wave) and ~2.5 TB/s for the exchange.  MARLIN_HIP_DENSE_PREFILL_SPLITS
+// forces a count.
+int dense_prefill_splits(int tiles, int nks, int cus) {
+  static const int forced = [] {
+    const char* e = getenv("MARLIN_HIP_DENSE_PREFILL_SPLITS");
+    const int x = e ? atoi(e) : 0;
+    return x >= 1 && x <= 16 ? x : 0;
+  }();
+  const int max_s = nks / 8;  // at least eight k-steps per split
+  if (forced) return forced < max_s ? forced : (max_s > 0 ? max_s : 1);
+  const double step_us = 1.3, exchange_bytes_per_us = 2.5e6;
+  int best_s = 1;
+  double best = 1e30;
+  for (int s = 1; s <= 8 && s <= max_s; s++) {
+    const long long rounds = ((long long)tiles * s + cus - 1) / cus;
+    const double traffic = s > 1 ? 2.0 * tiles * s * (double)kDpSplitBytes : 0.0;
+    const double cost = (double)rounds * step_us * nks / s + traffic / exchange_bytes_per_us;
+    if (cost < 0.97 * best) {
+      best = cost;
+      best_s = s;
+    }
+  }
+  if ((size_t)tiles * sizeof(uint32_t) > kCounterBytes) best_s = 1;
+  return best_s;
+}
+
+int run_dense_prefill(const void* A, const void* B, void* C, const void* s, int M, int N, int K, bool grouped,
+                      int dev, hipStream_t stream, int sms) {
+  DensePreArgs p{};
+  p.A = static_cast<const _Float16*>(A);
+  p.B = static_cast<const uint32_t*>(B);
+  p.s = static_cast<const _Float16*>(s);
+  p.C = static_cast<_Float16*>(C);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  const int tiles = (N / kDpTileCols) * ((M + kDpRows - 1) / kDpRows);
+  p.splits = dense_prefill_splits(tiles, K / 64, sms);
+  if (p.splits > 1) {
+    const int err = get_scratch(dev, stream, (size_t)tiles * p.splits * kDpSplitBytes, &p.counters, &p.partial);
+    if (err != MARLIN_HIP_OK) return err;
+    if (!p.counters) p.splits = 1;  // capturing, and this stream has no scratch yet
+  }
+  return launch_error(launch_dense_prefill(p, grouped, stream));
+}
+
 int run_dense(const void* A, const void* B, void* C, const void* s, int prob_m, int prob_n, int prob_k,
               int groupsize, int dev, hipStream_t stream, int thread_k, int thread_n, int sms) {
   int err = dense_validate(prob_m, prob_n, prob_k, groupsize, thread_k, thread_n);
@@ -296,6 +361,7 @@ int run_dense(const void* A, const void* B, void* C, const void* s, int prob_m, 
     if (hipDeviceGetAttribute(&sms, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || sms <= 0)
       sms = 256;
   }
+  if (dense_prefill_fits(M, N, K)) return run_dense_prefill(A, B, C, s, M, N, K, groupsize != -1, dev, stream, sms);
   const int bb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   const int ztiles = (M + 16 * bb - 1) / (16 * bb);
   const int chunks = N / 64;

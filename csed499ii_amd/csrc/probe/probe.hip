@@ -6,6 +6,10 @@
 //                       bytes, at the rate the memory system gives a plain read.
 //   marlin_probe_empty  an empty kernel on a given grid: the launch and dispatch cost
 //                       of a call on that grid.
+//   marlin_probe_mfma_32x32x16
+//                       one v_mfma_f32_32x32x16_f16 whose operands and result are
+//                       placed by the lane layout the dense large-M kernel assumes,
+//                       so that a test can compare it with the plain product.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,6 +42,28 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const u32x4* __restrict
 
 __global__ void probe_empty_kernel() {}
 
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// One wave.  Lane l = 32 hk + i: A operand = row i, k 8 hk .. 8 hk + 7 of A (32 x 16,
+// row-major); B operand = column i, the same k of B (16 x 32, row-major); result
+// register r = D[8 (r / 4) + 4 hk + r % 4][i] of D (32 x 32, row-major).
+__global__ __launch_bounds__(64) void probe_mfma_32x32x16_kernel(const _Float16* __restrict__ A,
+                                                                 const _Float16* __restrict__ B,
+                                                                 float* __restrict__ D) {
+  const int l = threadIdx.x, i = l & 31, hk = l >> 5;
+  half8_t a, b;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    a[e] = A[i * 16 + 8 * hk + e];
+    b[e] = B[(8 * hk + e) * 32 + i];
+  }
+  f32x16 c = {};
+  c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 16; r++) D[(8 * (r >> 2) + 4 * hk + (r & 3)) * 32 + i] = c[r];
+}
+
 }  // namespace
 
 extern "C" {
@@ -55,6 +81,13 @@ int marlin_probe_empty(int blocks, int threads, int dev, hipStream_t stream) {
   if (blocks <= 0 || threads <= 0 || threads > 1024) return 1;
   if (hipSetDevice(dev) != hipSuccess) return 3;
   hipLaunchKernelGGL(probe_empty_kernel, dim3((unsigned)blocks), dim3((unsigned)threads), 0, stream);
+  return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int marlin_probe_mfma_32x32x16(const void* A, const void* B, void* D, int dev, hipStream_t stream) {
+  if (hipSetDevice(dev) != hipSuccess) return 3;
+  hipLaunchKernelGGL(probe_mfma_32x32x16_kernel, dim3(1), dim3(64), 0, stream, static_cast<const _Float16*>(A),
+                     static_cast<const _Float16*>(B), static_cast<float*>(D));
   return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 

@@ -1,4 +1,5 @@
-/* C ABI of libmarlin_probe.so: measurement aids of bench.py's floor workload.  Not
+/* C ABI of libmarlin_probe.so: measurement aids of bench.py's floor workload and a
+ * lane-layout check of one MFMA instruction for the tests.  Not
  * part of the GEMM library and with no counterpart in the reference.  Return codes:
  * 0 ok, 1 bad argument, 3 HIP failure. */
 #ifndef MARLIN_PROBE_H
@@ -17,6 +18,11 @@ int marlin_probe_read(const void* p, long long bytes, void* sink, int blocks, in
 
 /* An empty kernel on `blocks` workgroups of `threads` threads. */
 int marlin_probe_empty(int blocks, int threads, int dev, hipStream_t stream);
+
+/* One v_mfma_f32_32x32x16_f16 on one wave with the operand and result lane layout
+ * the dense large-M kernel assumes: A 32 x 16 and B 16 x 32 fp16, D 32 x 32 fp32,
+ * all row-major device arrays.  D equals A @ B when the assumption holds. */
+int marlin_probe_mfma_32x32x16(const void* A, const void* B, void* D, int dev, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,9 +1,10 @@
-"""ISA checks of the large-M kernel (CPU; needs hipcc, no GPU).
+"""ISA checks of the large-M kernels (CPU; needs hipcc, no GPU).
 
-sm24_prefill_kernel issues its MFMAs as inline assembly (accumulators in AGPRs), so
-the compiler's hazard recognizer does not guard them.  These tests compile the
-kernel to gfx950 assembly and check, on every instantiation, the two rules the
-kernel relies on (the wait states hipcc itself inserts around the v_smfmac builtin):
+sm24_prefill_kernel (2:4) and marlin_dense_prefill_kernel (dense) issue their MFMAs
+as inline assembly (accumulators in AGPRs), so the compiler's hazard recognizer does
+not guard them.  These tests compile the kernels to gfx950 assembly and check, on
+every instantiation, the two rules the kernels rely on (the wait states hipcc itself
+inserts around the MFMA builtins):
 
 * a VALU write of a register that an smfmac reads (A, B, index or accumulator)
   lies at least 2 wait states before it;
@@ -24,6 +25,8 @@ import pytest
 
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 SRC = ROOT / "csed499ii_amd" / "csrc" / "sm24_prefill.hip"
+DENSE_SRC = ROOT / "csed499ii_amd" / "csrc" / "marlin_dense_prefill.hip"
+MFMA = ("v_smfmac", "v_mfma")
 
 
 def _regs(tok):
@@ -71,7 +74,7 @@ def hazards(body):
             tails[labels[ops[0]]] = k
     found = []
     for i, (op, s, ops) in enumerate(flat):
-        if not op.startswith("v_smfmac"):
+        if not op.startswith(MFMA):
             continue
         reads = set().union(*(_regs(o) for o in ops[:4]))
         window, w, j = [], 0, i - 1
@@ -86,12 +89,12 @@ def hazards(body):
                 w += _wait_states(flat[j][0], flat[j][2])
                 j -= 1
         for (pop, ps, pops), pw in window:
-            if pop.startswith("v_") and not pop.startswith("v_smfmac") and pops and _regs(pops[0]) & reads:
+            if pop.startswith("v_") and not pop.startswith(MFMA) and pops and _regs(pops[0]) & reads:
                 found.append(f"VALU write {pw} wait states before smfmac: {ps!r} -> {s!r}")
         dst, w, j = _regs(ops[0]), 0, i + 1
         while j < len(flat) and w < 8:
             nop, ns, nops = flat[j]
-            if nop.startswith("v_smfmac") and _regs(nops[0]) == dst:
+            if nop.startswith(MFMA) and _regs(nops[0]) == dst:
                 break
             if nop.startswith(("global_store", "buffer_store", "flat_store", "ds_write")):
                 rd = set().union(*(_regs(o) for o in nops)) if nops else set()
@@ -104,21 +107,30 @@ def hazards(body):
     return found
 
 
-def _kernels(asm):
-    return {m.group(1): m.group(0) for m in re.finditer(r"\n(_Z\w*sm24_prefill_kernel\w*):.*?s_endpgm", asm, re.S)}
+def _kernels(asm, name="sm24_prefill_kernel"):
+    return {m.group(1): m.group(0) for m in re.finditer(r"\n(_Z\w*" + name + r"\w*):.*?s_endpgm", asm, re.S)}
+
+
+def _compile(src, tmp_path_factory):
+    hipcc = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not pathlib.Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa") / (src.stem + ".s")
+    from csed499ii_amd import build
+    cmd = [hipcc, *build.compile_flags(), *build.EXTRA_FLAGS.get(src.name, []), "--cuda-device-only", "-S",
+           "-o", str(out), str(src)]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    return out.read_text()
 
 
 @pytest.fixture(scope="module")
 def prefill_asm(tmp_path_factory):
-    hipcc = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-    if not pathlib.Path(hipcc).exists():
-        pytest.skip("hipcc not available")
-    out = tmp_path_factory.mktemp("isa") / "prefill.s"
-    from csed499ii_amd import build
-    cmd = [hipcc, *build.compile_flags(), *build.EXTRA_FLAGS.get(SRC.name, []), "--cuda-device-only", "-S",
-           "-o", str(out), str(SRC)]
-    subprocess.run(cmd, check=True, capture_output=True, text=True)
-    return out.read_text()
+    return _compile(SRC, tmp_path_factory)
+
+
+@pytest.fixture(scope="module")
+def dense_prefill_asm(tmp_path_factory):
+    return _compile(DENSE_SRC, tmp_path_factory)
 
 
 def test_checker_catches_planted_hazards():
@@ -154,4 +166,21 @@ def test_prefill_registers(prefill_asm):
     # on a SIMD
     assert prefill_asm.count("; NumAgprs: 128") == 2
     for v in re.findall(r"; NumVgprs: (\d+)", prefill_asm):
+        assert int(v) <= 128
+
+
+def test_dense_prefill_mfma_hazards(dense_prefill_asm):
+    kernels = _kernels(dense_prefill_asm, "marlin_dense_prefill_kernel")
+    assert len(kernels) == 2  # grouped and per-column scales
+    for name, body in kernels.items():
+        assert sum(1 for l in body.split("\n") if "v_mfma_f32_32x32x16_f16" in l) >= 128, name
+        assert hazards(body) == [], name
+
+
+def test_dense_prefill_registers(dense_prefill_asm):
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", dense_prefill_asm, re.S):
+        body = m.group(2)
+        assert int(re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", body).group(1)) == 0, m.group(1)
+    assert dense_prefill_asm.count("; NumAgprs: 128") == 2
+    for v in re.findall(r"; NumVgprs: (\d+)", dense_prefill_asm):
         assert int(v) <= 128
