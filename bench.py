@@ -423,12 +423,16 @@ class SparseLtCall:
 def time_site(fn, reps=20, samples=5):
     """µs per call of ``fn``: a captured graph of ``reps`` calls, or (when the library
     call cannot be captured) ``reps`` eager calls between two events; median of
-    ``samples``.  Returns (µs, method)."""
-    fn()
+    ``samples``.  The warm-up call runs on the capture stream, so that a call that
+    splits K has that stream's scratch when it is captured.  Returns (µs, method)."""
+    s = capture_stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
     torch.cuda.synchronize()
     try:
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=s):
             for _ in range(reps):
                 fn()
         g.replay()
