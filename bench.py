@@ -860,7 +860,8 @@ def main():
         out["per_call"] = per_call_stats(pass_calls if not wl.startswith("stack") else pass_calls[:4])
     if wl == "decode" and not args.no_prefill:
         # the prefill half of the metric: Llama-2-70B shapes at M >= 512, TFLOP/s
-        pres, pcalls, pcfg = measure(args, "prefill", device, max(3, args.steps // 4), 2)
+        # 10 steps (~70 ms) after 3 warm-up steps: fewer read ~2 % low from run to run
+        pres, pcalls, pcfg = measure(args, "prefill", device, max(10, args.steps // 2), 3)
         proof = roofline_of("prefill", pres, pcalls)
         out["prefill"] = {"value": round(pres["tflops"], 1), "unit": "TFLOP/s", "steps": pres["steps"],
                           "warmup": pres["warmup"], "ms_per_step": pres["ms_per_step"],
