@@ -54,7 +54,11 @@ def test_reference_correctness_cases():
 @pytest.mark.parametrize("batch", [1, 2, 4, 8, 12, 16, 32, 64])
 @pytest.mark.parametrize("tile", [(64, 256), (128, 128)])
 def test_reference_tiles(batch, tile):
-    """test_2_4.py:95-101 (N=512, K=1024, g=-1)."""
+    """test_2_4.py:95-101 (N=512, K=1024, g=-1).  The reference's (thread_k, thread_m)
+    pick a CUDA kernel configuration; here they are checked against the reference's
+    rules (an unsupported pair raises, test_kernel_shape_errors_raise) and accepted
+    pairs give the same product, computed with the planner's own tile choice for
+    this GPU (the tile arguments do not select a kernel)."""
     if batch > 16 and tile == (128, 128):
         pytest.skip("the reference has no 128x128 kernel for more than one batch block")
     wt, A = _problem(batch, 512, 1024, -1, 10 + batch)
