@@ -315,8 +315,8 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   //   barrier: this wave's DMAs of step s+1 have landed, every wave has finished step
   //   s-1 (its reads of slot Q+3);
   //   16 regions r = (kb, rg, hf), each one MFMA plus a share of: DMA group r >> 1 of
-  //   step s+3 (r = 1, 3); at hf = 0 the read of B fragment f+2 (f = 4kb + rg; from
-  //   step s+1 past 7); at r < 2 the raw words and metadata of step s+1, k-block r,
+  //   step s+3 (r = 1, 3); at hf = 0 the read of B fragment f+3 (f = 4kb + rg; from
+  //   step s+1 past 7; its ring slot held fragment f-1, used up by then); at r < 2 the raw words and metadata of step s+1, k-block r,
   //   and at r = 2 its scales; at r >= 2 slice (r-2) % 7 of dequantizing k-block
   //   (r-2) / 7 of step s+1.
   // Steps past the last are skipped (uniform); the DMAs are clamped, so the vmcnt of
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
       if (hf) pre_smfmac<1>(acc[rg][hf], av[P][kb][hf], bv[f & 3], ix[P][kb]);
       else pre_smfmac<0>(acc[rg][hf], av[P][kb][hf], bv[f & 3], ix[P][kb]);
       __builtin_amdgcn_sched_barrier(0);  // the region's work follows its MFMA
-      if (hf == 0) bv[(f + 2) & 3] = read_b(f + 2 < 8 ? Q : QN, (f + 2) & 7);
+      if (hf == 0) bv[(f + 3) & 3] = read_b(f + 3 < 8 ? Q : QN, (f + 3) & 7);
       if (r == 1 || r == 3) dma(s + 3, QD, r >> 1);
       if (r < 2) read_raw(QN, r);
       if (r == 2) read_scales(QN);
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   };
 
   // ---- prologue: DMAs of steps 0..2, then step 0's operands dequantized and its first
-  // two B fragments read ----
+  // three B fragments read ----
 #pragma unroll
   for (int s = 0; s < 3; s++)
 #pragma unroll
@@ -355,6 +355,7 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
     for (int sl = 0; sl < 7; sl++) dq_slice(kb, sl, 0);
   bv[0] = read_b(0, 0);
   bv[1] = read_b(0, 1);
+  bv[2] = read_b(0, 2);
   __builtin_amdgcn_sched_barrier(0);
 
   const int nls = ks1 - ks0;  // k-steps of this split (even)
