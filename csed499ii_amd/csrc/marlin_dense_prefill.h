@@ -30,7 +30,7 @@
 // Issue schedule.  Each k-tile is 8 regions (rg, hf), one MFMA each; beside them the
 // next k-tile's two A fragments are dequantized in seven slices of at most four VALU
 // instructions (regions 0-6: the operands are finished at least two instructions
-// before the first MFMA that reads them), the next k-tile's B fragments are read two
+// before the first MFMA that reads them), the next k-tile's B fragments are read three
 // fragments ahead, the raw words two k-tiles ahead, and the DMAs of the step three
 // ahead are issued in the step's first regions.
 #pragma once
@@ -313,7 +313,8 @@ __global__ __launch_bounds__(kDpThreads, 1) void marlin_dense_prefill_kernel(Den
   //   barrier: this wave's DMAs of step s + 1 have landed, every wave has finished
   //   step s - 1 (its reads of slot QD);
   //   k-tile kt, region r = (rg, hf): MFMA (kt, rg, hf); at hf = 0 the read of B
-  //   fragment f + 2 (f = 4 kt + rg; from step s + 1 past 15); at r = 0 the raw codes
+  //   fragment f + 3 (f = 4 kt + rg; from step s + 1 past 15; its ring slot held
+  //   fragment f - 1, used up by then); at r = 0 the raw codes
   //   of k-tile kt + 2 (from step s + 1 past 3) and, at kt = 2, the scales of step
   //   s + 1; at r < 7 slice r of dequantizing k-tile kt + 1 (with step s + 1's scales
   //   at kt = 3); at kt = 0, r = 1, 3 the DMA groups of step s + 3.
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(kDpThreads, 1) void marlin_dense_prefill_kernel(Den
         const int rg = r >> 1, hf = r & 1, f = 4 * kt + rg;
         dp_mfma(acc[rg][hf], av[P][hf], bv[f & 3]);
         __builtin_amdgcn_sched_barrier(0);  // the region's work follows its MFMA
-        if (hf == 0) bv[(f + 2) & 3] = read_b(f + 2 < 16 ? Q : QN, (f + 2) & 15);
+        if (hf == 0) bv[(f + 3) & 3] = read_b(f + 3 < 16 ? Q : QN, (f + 3) & 15);
         if (r == 0) read_raw(kt + 2 < 4 ? Q : QN, (kt + 2) & 3, P);
         if (r == 0 && kt == 2) read_scales(QN, SP ^ 1);
         if (kt == 0 && (r == 1 || r == 3)) dma(s + 3, QD, r >> 1);
@@ -341,7 +342,7 @@ __global__ __launch_bounds__(kDpThreads, 1) void marlin_dense_prefill_kernel(Den
   };
 
   // ---- prologue: DMAs of steps 0..2; step 0's scales, k-tile 0 dequantized, raw codes
-  // of k-tile 1, the first two B fragments ----
+  // of k-tile 1, the first three B fragments ----
 #pragma unroll
   for (int s = 0; s < 3; s++)
 #pragma unroll
@@ -354,6 +355,7 @@ __global__ __launch_bounds__(kDpThreads, 1) void marlin_dense_prefill_kernel(Den
   read_raw(0, 1, 1);
   bv[0] = read_b(0, 0);
   bv[1] = read_b(0, 1);
+  bv[2] = read_b(0, 2);
   __builtin_amdgcn_sched_barrier(0);
 
   const int nls = ks1 - ks0;  // k-steps of this split (even)
