@@ -409,7 +409,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
         }
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++) acc[q2][cb][rb] = smfmac64<0>(aop, act[rb], acc[q2][cb][rb], idx);
+        for (int rb = 0; rb < RB; rb++) {
+          acc[q2][cb][rb] = smfmac64<0>(aop, act[rb], acc[q2][cb][rb], idx);
+          // 64-column tiles: keep each accumulator in one register set across the
+          // unrolled stages (without this pin the register allocator alternates two
+          // sets and copies every accumulator once per stage: 3 v_mov per MFMA)
+          if constexpr (TC == 64) asm volatile("" : "+v"(acc[q2][cb][rb]));
+        }
       }
     }
   };

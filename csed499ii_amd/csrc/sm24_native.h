@@ -279,6 +279,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs 
         }
         if (j & 1) acc[j][cb] = smfmac64<1>(aop, act[j], acc[j][cb], xv[j >> 1]);
         else acc[j][cb] = smfmac64<0>(aop, act[j], acc[j][cb], xv[j >> 1]);
+        asm volatile("" : "+v"(acc[j][cb]));
       }
     }
     __builtin_amdgcn_wave_barrier();  // the slot's reads are issued before the next quad's writes

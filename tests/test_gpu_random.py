@@ -1,5 +1,5 @@
 """Seeded random shapes through every GEMM entry point (4-bit, 3-bit metadata, 3-bit
-values, lane-native) against the CPU oracle: ragged batches across the decode,
+values, lane-native, dense) against the CPU oracle: ragged batches across the decode,
 chunked-decode, general and large-M paths, both scale modes."""
 import random
 
@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from csed499ii_amd import marlin, synth
+from oracle import sm24_oracle as o
 from tests.gpu_util import assert_close, oracle_gemm, to_cpu
 
 pytestmark = pytest.mark.gpu
@@ -48,3 +49,29 @@ def test_random_shapes_against_oracle(kind, M, N, K, g):
         marlin.mul_2_4_native(A, Bn, Mn, C, Sn)
     torch.cuda.synchronize()
     assert_close(C.cpu().numpy(), oracle_gemm(A.cpu().numpy(), to_cpu(wt)), f"{kind} M={M} N={N} K={K} g={g}")
+
+
+def _dense_cases(seed, n):
+    rng = random.Random(seed)
+    out = []
+    for _ in range(n):
+        g = rng.choice([128, -1])
+        M = rng.choice([1, 2, 7, 16, 31, 48, 65, 100, 129, 200, 333])
+        N = rng.choice([256, 512, 768, 1024, 1536, 2048])
+        K = 128 * (rng.choice([1, 2, 3, 8, 17, 40]) if g == 128 else rng.choice([1, 2, 4, 9]))
+        out.append((M, N, K, g))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,g", _dense_cases(20261202, 20))
+def test_random_dense_shapes_against_oracle(M, N, K, g):
+    """The dense op (reference marlin/__init__.py:61-75) on seeded shapes that cross
+    its small-batch and large-M kernels, with and without split-K."""
+    wt = synth.make_dense_weight(K, N, M * 5 + K + N, g, device=DEV)
+    A = synth.make_activation(M, K, M + N + 3, device=DEV)
+    C = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    ws = torch.zeros(max(N // 128 * 16, 16), dtype=torch.int32, device=DEV)
+    marlin.mul(A, wt["B"], C, wt["s"], ws)
+    torch.cuda.synchronize()
+    W = o.dense_dequant(wt["B"].cpu().numpy(), wt["s"].cpu().numpy(), K, N, g)
+    assert_close(C.cpu().numpy(), o.gemm(A.cpu().numpy(), W), f"dense M={M} N={N} K={K} g={g}")
