@@ -301,6 +301,44 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // st: the wave's stage buffer; dact: direct activation operands; aoff: byte offset
   // of the stage in the resident rows
   auto compute = [&](const uint8_t* st, const half8_t* dact, uint32_t aoff) {
+    // 4-bit path: every LDS operand of the stage is read before the first is used
+    // (the larger batches run one or two waves per SIMD, where a read per use
+    // exposes its whole latency)
+    constexpr bool HOIST = VF == VAL4 && MF == META4;
+    uint32_t xr[KP][NCB][2];
+    u32x2 mr[KP][NCB];
+    _Float16 sr[NCB];
+    if constexpr (HOIST) {
+      if constexpr (MB < 16) {
+#pragma unroll
+        for (int q2 = 0; q2 < KP; q2++) {
+          if constexpr (RES) {
+            if (rho < M) {
+              const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
+              sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
+              sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(ap + 64);
+            }
+          } else if (rho < MB) {
+            sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
+            sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
+          }
+        }
+      }
+#pragma unroll
+      for (int q2 = 0; q2 < KP; q2++)
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+          const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
+          xr[q2][cb][0] = *reinterpret_cast<const uint32_t*>(vp);
+          xr[q2][cb][1] = *reinterpret_cast<const uint32_t*>(vp + 16);
+          mr[q2][cb] = *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
+        }
+      if constexpr (GROUPED) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) sr[cb] = *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int q2 = 0; q2 < KP; q2++) {
       half16_t act[RB];
@@ -308,7 +346,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         // Only lanes of real batch rows read the staged row; the other lanes' MFMA
         // columns are never stored, so their operand keeps whatever the register
         // held (LDS reads are paid per active lane).
-        if constexpr (RES) {
+        if constexpr (HOIST) {
+        } else if constexpr (RES) {
           if (rho < M) {
             const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
             sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
@@ -336,8 +375,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         if constexpr (VF == VAL4) {
           // words t0 and t0+1 of the lane's k-block row
           const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
-          const uint32_t x0 = *reinterpret_cast<const uint32_t*>(vp) >> nsh;
-          const uint32_t x1 = *reinterpret_cast<const uint32_t*>(vp + 16) >> nsh;
+          const uint32_t x0 = (HOIST ? xr[q2][cb][0] : *reinterpret_cast<const uint32_t*>(vp)) >> nsh;
+          const uint32_t x1 = (HOIST ? xr[q2][cb][1] : *reinterpret_cast<const uint32_t*>(vp + 16)) >> nsh;
           lo0 = (x0 & kMask) | kMagic;
           lo1 = (x1 & kMask) | kMagic;
           hi0 = (x0 & kMaskHi) | kMagic;
@@ -372,7 +411,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         // unit 16*jb + 2*gt + jj
         uint32_t idx;
         if constexpr (MF == META4) {
-          const u32x2 unit = *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
+          const u32x2 unit =
+              HOIST ? mr[q2][cb] : *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
           idx = __builtin_amdgcn_perm(unit.y, unit.x, msel);
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
@@ -405,7 +445,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           }
         }
         if constexpr (GROUPED) {
-          const _Float16 sc = *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
+          const _Float16 sc = HOIST ? sr[cb] : *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
           aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
         }
 #pragma unroll
