@@ -552,12 +552,12 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 // 11008x4096 at M = 8: 9.13 -> 8.84 us; o 4096x4096 at M = 32: 8.46 -> 7.83 us).
 // Wider N takes 64-column tiles from M = 8, below that 32-column tiles when N/32 is at
 // least twice the CU count, else 16.  A split costs a hand-off through the uncached
-// scratch (>= 2.5 us), so it is used only where measured to pay.  Long K (>= 8192)
-// at wider N splits K four ways at N <= 10240 (Llama-2-70B qkv, down) and two ways
-// for the widest N from M = 2; Llama-2-70B o (N/16 = 2 per CU) keeps 32-column tiles
-// unsplit up to M = 8 (8.55 -> 7.47 us at M = 1).  7B sweep (M in {1, 2, 4, 8, 16}):
-// 162.4 us summed over the 20 calls, against 168.0 us for the previous kernel, whose
-// LDS stages were shared by the workgroup behind a barrier, on its own table.
+// scratch (>= 2.5 us), so it is used only where measured to pay.  Long K (>= 8192):
+// the widest N (Llama-2-70B gate_up) runs unsplit up to 8 rows (M = 4: 41.5 -> 38.5
+// us against two splits) and splits in two beyond; N <= 10240 (qkv, down) splits K
+// four ways (down at M = 1 two ways: 20.3 -> 19.4 us); Llama-2-70B o (N/16 = 2 per
+// CU) keeps 32-column tiles unsplit up to M = 8 (8.55 -> 7.47 us at M = 1).  The 7B
+// sweep (M in {1, 2, 4, 8, 16}) is within noise of the best forced choice per call.
 // MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
 struct DecodeShape {
   int tc, nw, splits;
@@ -577,13 +577,22 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
     else if (longk && M > 4) d = {64, 8, 4};
     else d = {16, M <= 4 ? 8 : 4, 1};
   } else if (longk) {
-    // long K at wide N (the Llama-2-70B shapes): K splits of 64-column tiles; 32-column
+    // long K at wide N (the Llama-2-70B shapes): unsplit tiles where N alone fills the
+    // CUs (the widest N up to 8 rows), K splits of 64-column tiles otherwise; 32-column
     // tiles for few rows where N/16 fills one round of two per CU.
-    if (wide32) d = M == 1 ? DecodeShape{32, 4, 1} : DecodeShape{64, 4, 2};
-    else if (M > 8) d = {64, 4, 4};
-    else if (K >= 16384) d = {64, 8, 4};
-    else if (N / 16 <= 2 * cus) d = {32, 8, 1};
-    else d = {M <= 4 ? 32 : 64, 4, 4};
+    if (wide32) {
+      if (M == 1) d = {32, 8, 1};
+      else if (M <= 8) d = {64, M <= 4 ? 4 : 8, 1};
+      else d = {64, 4, 2};
+    } else if (M > 8) {
+      d = {64, 4, 4};
+    } else if (K >= 16384) {
+      d = M == 1 ? DecodeShape{64, 8, 2} : M <= 4 ? DecodeShape{64, 4, 4} : DecodeShape{64, 8, 4};
+    } else if (N / 16 <= 2 * cus) {
+      d = {32, 8, 1};
+    } else {
+      d = {M <= 4 ? 32 : 64, 4, 4};
+    }
   } else if (M > 16) {
     d = {64, 4, N / 64 >= cus ? 2 : 1};
   } else if (M >= 8) {
