@@ -1,8 +1,9 @@
 // Decode-sized (M <= 32) 2:4 INT4 x FP16 GEMM for gfx950.
 //
 // One workgroup owns a tile of TC output columns (TC = 16, 32 or 64) over the whole
-// K, or over one of a.splits contiguous ranges of its stages (split-K: the host sums
-// the ranges through its scratch).  Unsplit, the result never crosses workgroups: a
+// K, or over one of a.splits contiguous ranges of its stages (split-K, of every tile
+// or of the tiles past a.tail_from: the last split to arrive sums the ranges through
+// the host's scratch).  Unsplit, the result never crosses workgroups: a
 // cross-workgroup hand-off costs microseconds on this multi-XCD part, more than the
 // whole weight stream of a 4096x4096 layer.
 //
@@ -100,20 +101,38 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const int N = a.N, K = a.K, M = a.M;
   const int nkb = K >> 5;
   const int ngroups = (nkb + 3) >> 2;
-  // Split-K: block b = z * ntiles + tile; split z covers stages [st0, st1) of the tile
-  // (the host keeps splits <= the stage count).
-  // Without a split (the usual case) no division runs: a 64-bit or even a 32-bit
-  // division is a long scalar chain that every wave would pay before its first load.
+  // Split-K: split z of a tile covers stages [st0, st0 + nst) (the host keeps splits
+  // <= the stage count).  Every tile split (a.tail_from == 0): block b = z * ntiles +
+  // tile.  Tail split (a.tail_from = T0 > 0): blocks b < T0 own the whole K of tile
+  // b; the remaining ntiles - T0 tiles are split, block T0 + S * p + z running split
+  // z of tile T0 + p, so that the few tiles past one per CU spread over all CUs
+  // instead of doubling the load of some.  Without a split (the usual case) no
+  // division runs: a 64-bit or even a 32-bit division is a long scalar chain that
+  // every wave would pay before its first load.
   const int ntiles = N / TC;
-  const int S = a.splits;
+  int S = 1;                          // splits of this workgroup's tile
   const int nst_all = (nkb + KS - 1) / KS;
   int z = 0, st0 = 0, nst = nst_all;  // split z covers stages [st0, st0 + nst)
   int tile = blockIdx.x;
-  if (S > 1) {  // uniform; nst_all * S is small, so 32 bits are exact
-    z = (int)((unsigned)blockIdx.x / (unsigned)ntiles);
-    tile -= z * ntiles;
-    st0 = (int)((unsigned)(nst_all * z) / (unsigned)S);
-    nst = (int)((unsigned)(nst_all * (z + 1)) / (unsigned)S) - st0;
+  int ptile = 0;                      // index of the tile among the split tiles
+  if (a.splits > 1) {  // uniform; nst_all * S is small, so 32 bits are exact
+    const int T0 = a.tail_from;
+    if (T0 == 0) {
+      S = a.splits;
+      z = (int)((unsigned)blockIdx.x / (unsigned)ntiles);
+      tile -= z * ntiles;
+      ptile = tile;
+    } else if ((int)blockIdx.x >= T0) {
+      S = a.splits;
+      const unsigned j = blockIdx.x - (unsigned)T0;
+      ptile = (int)(j / (unsigned)S);
+      z = (int)j - ptile * S;
+      tile = T0 + ptile;
+    }
+    if (S > 1) {
+      st0 = (int)((unsigned)(nst_all * z) / (unsigned)S);
+      nst = (int)((unsigned)(nst_all * (z + 1)) / (unsigned)S) - st0;
+    }
   }
   // XCD-aware tile order.  Workgroups are dispatched round-robin over the 8 XCDs
   // (block b runs on XCD b % 8) and each XCD has its own L2.  The SUB = 64/TC tiles of
@@ -537,7 +556,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   };
   // partial of (tile, split, rb): 16 x TC floats in row-major order
   auto partial_at = [&](int zz, int rb) -> float* {
-    return a.partial + ((size_t)(tile * S + zz) * RB + rb) * (16 * TC) + r_out * TC + c_out;
+    return a.partial + ((size_t)(ptile * S + zz) * RB + rb) * (16 * TC) + r_out * TC + c_out;
   };
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {

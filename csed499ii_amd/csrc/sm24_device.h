@@ -109,6 +109,7 @@ struct GemmArgs {
   const _Float16* zeros;  // >= 64 zero bytes (activation rows that do not exist)
   int M, N, K;
   int splits;
+  int tail_from;   // decode: first split tile (0: every tile split when splits > 1)
   float* partial;  // [splits][M][N] when splits > 1
   uint32_t* counters;  // [gridDim.z][gridDim.x] arrival counters, zero between launches
 };

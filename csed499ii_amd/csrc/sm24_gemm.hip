@@ -561,7 +561,8 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 // MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
 struct DecodeShape {
   int tc, nw, splits;
-  bool deep;  // register ring: deep (more stages in flight) or 16 VGPRs
+  bool deep;          // register ring: deep (more stages in flight) or 16 VGPRs
+  int tail_from = 0;  // > 0: only the tiles from this one are split (tail split)
 };
 bool decode_deep(int K, int splits);
 DecodeShape decode_shape(int M, int N, int K, int cus) {
@@ -609,9 +610,37 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   const int kpw = 64 / d.tc > 2 ? 64 / d.tc : 2;
   const int nst = (K / 32 + d.nw * kpw - 1) / (d.nw * kpw);
   if (d.splits > nst) d.splits = nst;
-  if ((size_t)(N / d.tc) * sizeof(uint32_t) > kCounterBytes) d.splits = 1;
-  d.deep = decode_deep(K, d.splits);
+  // Tail split: with q whole rounds of tiles over the CUs and a tail of f <= CUs/2
+  // tiles left over, the tail tiles are split S = min(4, CUs/f) ways, so that every
+  // CU runs q whole tiles plus at most one piece instead of q + 1 whole tiles on f of
+  // them (the pieces' hand-off overlaps the whole tiles).  7B gate_up 4096x22016 at
+  // M = 8 and 16 (344 tiles on 256 CUs): 12.0 -> 11.0 and 13.7 -> 12.5 us; three
+  // ways (264 pieces, more than the CUs) 13.0 and 13.7.  MARLIN_HIP_DECODE_TAIL
+  // forces S (0: off).
+  static const int forced_tail = env_choice("MARLIN_HIP_DECODE_TAIL", {0, 2, 3, 4}, -1);
+  const int ntiles = N / d.tc;
+  if (d.splits == 1 && forced_tail != 0 && cus > 0 && ntiles > cus) {
+    const int q = ntiles / cus, f = ntiles - q * cus;
+    int st = forced_tail > 0 ? forced_tail : (2 * f <= cus && f > 0 ? cus / f : 1);
+    if (st > 4) st = 4;
+    if (st > nst) st = nst;
+    if (st > 1 && f > 0) {
+      d.tail_from = q * cus;
+      d.splits = st;
+    }
+  }
+  if ((size_t)ntiles * sizeof(uint32_t) > kCounterBytes) {
+    d.splits = 1;
+    d.tail_from = 0;
+  }
+  d.deep = decode_deep(K, d.tail_from > 0 ? 1 : d.splits);
   return d;
+}
+
+// Workgroups of a decode launch.
+int decode_workgroups(int N, const DecodeShape& d) {
+  const int ntiles = N / d.tc;
+  return d.tail_from > 0 ? d.tail_from + (ntiles - d.tail_from) * d.splits : ntiles * d.splits;
 }
 
 // Register ring depth: shallow (16 VGPRs: more resident workgroups) up to 16384 k per
@@ -627,6 +656,7 @@ bool decode_deep(int K, int splits) {
 // The same decode shape without a K split (no split-K scratch available or wanted).
 void decode_unsplit(DecodeShape& d, int K) {
   d.splits = 1;
+  d.tail_from = 0;
   d.deep = decode_deep(K, 1);
 }
 
@@ -652,11 +682,13 @@ constexpr size_t kDecodeLdsMax = 64 * 1024;
 template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
 void launch_decode_v(const GemmArgs& a, hipStream_t stream) {
   static const int forced_res = env_choice("MARLIN_HIP_DECODE_RES", {0, 1}, 1);
-  const dim3 grid(a.N / TC * a.splits), block(64 * NW);
+  const int ntiles = a.N / TC;
+  const dim3 grid(a.tail_from > 0 ? a.tail_from + (ntiles - a.tail_from) * a.splits : ntiles * a.splits);
+  const dim3 block(64 * NW);
   if constexpr (MB < 16) {
     constexpr int ks = NW * (64 / TC > 2 ? 64 / TC : 2);
     const int nst_all = (a.K / 32 + ks - 1) / ks;
-    const int nst_max = (nst_all + a.splits - 1) / a.splits;
+    const int nst_max = a.tail_from > 0 ? nst_all : (nst_all + a.splits - 1) / a.splits;
     const size_t dyn = (size_t)MB * ((size_t)nst_max * ks * 64 + 16);
     static const size_t stat =
         static_lds(reinterpret_cast<const void*>(&sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>));
@@ -781,7 +813,7 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
     const int mc = M < kDecodeMaxM ? M : kDecodeMaxM;
     DecodeShape d = decode_shape(mc, N, K, sms);
     if (noalloc) decode_unsplit(d, K);
-    out[1] = N / d.tc * d.splits;
+    out[1] = decode_workgroups(N, d);
     out[2] = 64 * d.nw;
     out[3] = d.splits;
     out[4] = (M + kDecodeMaxM - 1) / kDecodeMaxM;
@@ -856,12 +888,14 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       if (noalloc) decode_unsplit(shape, K);
       if (shape.splits > 1) {
         const int rows = decode_batch(mc) > 16 ? decode_batch(mc) : 16;
-        err = get_scratch(dev, stream, (size_t)(N / shape.tc) * shape.splits * rows * shape.tc * sizeof(float),
-                          &d.counters, &d.partial);
+        const size_t split_tiles = (size_t)(N / shape.tc - shape.tail_from);
+        err = get_scratch(dev, stream, split_tiles * shape.splits * rows * shape.tc * sizeof(float), &d.counters,
+                          &d.partial);
         if (err != MARLIN_HIP_OK) return err;
         if (!d.counters) decode_unsplit(shape, K);  // capturing, and this stream has no scratch yet
       }
       d.splits = shape.splits;
+      d.tail_from = shape.tail_from;
       err = launch_error(launch_decode(d, shape, vf, mf, groupsize != -1, stream));
       if (err != MARLIN_HIP_OK) return err;
     }

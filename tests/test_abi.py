@@ -95,7 +95,8 @@ def test_plan_without_gpu(built_lib):
     p = marlin.plan_2_4(1, 4096, 4096)
     assert p["kernel"] == "decode" and p["splits"] == 1 and p["launches"] == 1
     assert p["workgroups"] * (p["threads"] // 64) > 0
-    assert marlin.plan_2_4(16, 4096, 22016)["splits"] == 1
+    p = marlin.plan_2_4(16, 4096, 22016, sms=256)  # 344 tiles: the 88 past one per CU split in two
+    assert p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
     p = marlin.plan_2_4(24, 4096, 22016)  # wide N above 16 rows: 64-column tiles split in two
     assert p["kernel"] == "decode" and p["splits"] == 2 and p["workgroups"] == 22016 // 64 * 2
     assert marlin.plan_2_4(24, 4096, 22016, noalloc=True)["splits"] == 1

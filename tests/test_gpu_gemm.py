@@ -210,6 +210,29 @@ def test_deterministic_repeats():
         assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
+@pytest.mark.parametrize("M", [8, 12, 16])
+def test_decode_tail_split(M):
+    """Tail split: 4096x22016 has 344 64-column tiles at 8 to 16 rows, 88 past one
+    per CU; those 88 are split in two (workgroups 256 + 2 * 88) while the first 256
+    run whole. Column slices on both sides of the boundary (chunks 254-257), in the
+    middle of the split tiles and at the end match the oracle, and repeated calls
+    are bit-identical."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip("the tile counts of this case assume 256 CUs")
+    p = marlin.plan_2_4(M, 4096, 22016, sms=cus)
+    assert p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
+    wt, A = _problem(M, 22016, 4096, 128, 4242 + M)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    for _ in range(3):
+        assert torch.equal(_run(wt, A), C), "repeated tail-split calls differ"
+    t = to_cpu(wt)
+    for c0 in (254, 300, 340):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"tail split M={M} chunks {c0}..{c0 + 3}")
+
+
 @pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (24, 4096, 22016)])
 def test_graph_replay_matches_eager(M, K, N):
     """Captured calls replay the eager result bit for bit: 8 rows on 4096x4096 (one
