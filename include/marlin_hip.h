@@ -15,9 +15,11 @@
  * pointers): A M*K halves, B K*N/16 int32, meta K*N/16 int16, C M*N halves,
  * s (K/128 or 1)*N halves.
  *
- * The planner may split K (decode calls at wide N or long K, large-M calls with few
- * column tiles, lane-native calls at 5-16 rows whose tiles cover too few compute
- * units, and at 2-4 rows when K >= 16384).  The split-K scratch (fp32 partials and
+ * The planner may split K (decode calls at wide N or long K, decode calls whose
+ * column tiles leave a tail of at most half the compute units past whole rounds,
+ * where only the tail tiles are split, large-M calls with few column tiles,
+ * lane-native calls at 5-16 rows whose tiles cover too few compute units, and at
+ * 2-4 rows when K >= 16384).  The split-K scratch (fp32 partials and
  * arrival counters) is uncached device memory that the library allocates per
  * (device, stream), grows on demand and never frees; the operand staging buffer of
  * the 3-bit variants at large M and of the lane-native layout above 16 rows is kept
