@@ -233,13 +233,14 @@ def test_decode_tail_split(M):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"tail split M={M} chunks {c0}..{c0 + 3}")
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (24, 4096, 22016)])
+@pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (24, 4096, 22016), (16, 4096, 22016)])
 def test_graph_replay_matches_eager(M, K, N):
     """Captured calls replay the eager result bit for bit: 8 rows on 4096x4096 (one
-    16-column tile per workgroup, unsplit) and 24 rows on 4096x22016 (K split in two
-    through the capture stream's scratch, which the eager call on that stream made
-    first)."""
-    if M == 24:
+    16-column tile per workgroup, unsplit), 24 rows on 4096x22016 (every tile's K
+    split in two) and 16 rows on it (only the tail tiles past one round over the CUs
+    split), both through the capture stream's scratch, which the eager call on that
+    stream made first."""
+    if M > 8:
         assert marlin.plan_2_4(M, K, N)["splits"] == 2
     wt, A = _problem(M, N, K, 128, 9)
     ws = torch.zeros(N // 128 * 16, dtype=torch.int32, device=DEV)

@@ -87,6 +87,7 @@ def test_capture_on_fresh_stream_runs_unsplit():
     """A split-K call captured on a stream that has never run a call cannot allocate
     that stream's scratch: it is captured without a K split.  Replays match the
     unsplit (no-allocation) product bit for bit and the oracle within tolerance."""
+    assert marlin.plan_2_4(16, 4096, 22016)["splits"] > 1  # the eager plan splits K (tail tiles)
     wt = synth.make_weight(4096, 22016, 511, 128, device=DEV)
     A = synth.make_activation(16, 4096, 512, device=DEV)
     C_unsplit = torch.empty(16, 22016, dtype=torch.half, device=DEV)
