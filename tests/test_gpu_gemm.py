@@ -233,6 +233,27 @@ def test_decode_tail_split(M):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"tail split M={M} chunks {c0}..{c0 + 3}")
 
 
+@pytest.mark.parametrize("M,K,N,splits,wgs", [(1, 4096, 8704, 4, 640), (3, 4096, 8704, 4, 640),
+                                             (5, 4096, 8704, 4, 640), (8, 2048, 18432, 4, 384),
+                                             (12, 4096, 16896, 4, 288)])
+def test_decode_tail_split_shapes(M, K, N, splits, wgs):
+    """Tail split across the decode kernel's forms: 16-column tiles with resident
+    activation rows (M = 1, 3) and with direct 16-row operands (M = 5), the XCD
+    chunk remap (544 tiles, a multiple of 32), 64-column tiles (M = 8, 12); 32 or 8
+    tiles past the whole rounds, split four ways. The whole output matches the
+    oracle and repeated calls are bit-identical."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip("the tile counts of this case assume 256 CUs")
+    p = marlin.plan_2_4(M, K, N, sms=cus)
+    assert p["splits"] == splits and p["workgroups"] == wgs
+    wt, A = _problem(M, N, K, 128, 5150 + M + N)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    assert torch.equal(_run(wt, A), C), "repeated tail-split calls differ"
+    _check(wt, A, C, f"tail split M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (24, 4096, 22016), (16, 4096, 22016)])
 def test_graph_replay_matches_eager(M, K, N):
     """Captured calls replay the eager result bit for bit: 8 rows on 4096x4096 (one
