@@ -411,10 +411,14 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
           const uint32_t y0 = __builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3) + 6 * blk);
           const uint32_t y1 = __builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3) + 6 * blk);
-          lo0 = ((y0 & 0x7000u) << 4) | (y0 & 0x7u) | kMagic;
-          lo1 = ((y1 & 0x7000u) << 4) | (y1 & 0x7u) | kMagic;
-          hi0 = ((y0 & 0x38000u) << 5) | ((y0 & 0x38u) << 1) | kMagic;
-          hi1 = ((y1 & 0x38000u) << 5) | ((y1 & 0x38u) << 1) | kMagic;
+          // One 24-bit multiply moves both codes of a half pair at once: the masked
+          // fields (bits 0-2 and 12-14; 3-5 and 15-17) times 1 + 2^4 (2^1 + 2^5) land
+          // at bits 0-2 and 16-18 (4-6 and 20-22), and the other copies of the
+          // product fall outside the mask, with no carries between them.
+          lo0 = (__umul24(y0 & 0x7007u, 17u) & 0x00070007u) | kMagic;
+          lo1 = (__umul24(y1 & 0x7007u, 17u) & 0x00070007u) | kMagic;
+          hi0 = (__umul24(y0 & 0x38038u, 34u) & 0x00700070u) | kMagic;
+          hi1 = (__umul24(y1 & 0x38038u, 34u) & 0x00700070u) | kMagic;
         }
         constexpr float zp = VF == VAL4 ? 1032.0f : 1028.0f;  // 1024 + zero point
         constexpr float zh = (zp - 1024.0f) + 64.0f;          // the same for 1024 + 16 q, over 16
