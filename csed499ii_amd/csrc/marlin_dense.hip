@@ -269,11 +269,26 @@ hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// K splits: enough workgroups for two per compute unit, each wave keeping at least
-// two k-steps, at most 16 splits and one arrival counter per (chunk, batch tile).
+// K splits, from forced splits 1-16 over the Llama-2-7B decode calls (MI355X): a
+// split's hand-off costs microseconds, so tiles that already cover at least 3/4 of
+// the CUs run unsplit (qkv, 192 chunks: 16.0 -> 13.8 us at M = 1 against three
+// splits); fewer tiles split to about one workgroup per CU (o and down, 64 chunks:
+// four splits, 9.9 -> 9.0 and 12.7 -> 12.2 us against eight); between one and two
+// tiles per CU split in two, which balances the CUs (gate_up, 344 chunks: 20.7
+// against 22.3 us unsplit).  Each wave keeps at least two k-steps; at most 16
+// splits and one arrival counter per (chunk, batch tile).  MARLIN_HIP_DENSE_SPLITS
+// forces the count.
 int dense_splits(int chunks, int ztiles, int nks, int cus) {
+  static const int forced = [] {
+    const char* e = getenv("MARLIN_HIP_DENSE_SPLITS");
+    const int x = e ? atoi(e) : 0;
+    return x >= 1 && x <= 16 ? x : 0;
+  }();
   const long long tiles = (long long)chunks * ztiles;
-  int s = (int)((2LL * cus + tiles - 1) / tiles);
+  int s = 1;
+  if (forced) s = forced;
+  else if (tiles >= cus) s = tiles < 2LL * cus ? 2 : 1;
+  else if (4 * tiles < 3LL * cus) s = (int)((cus + tiles / 2) / tiles);
   const int smax = nks / 8 > 0 ? nks / 8 : 1;
   if (s > smax) s = smax;
   if (s > 16) s = 16;
