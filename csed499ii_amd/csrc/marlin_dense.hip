@@ -106,16 +106,31 @@ __global__ __launch_bounds__(64 * NW) void marlin_dense_kernel(DenseArgs a) {
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) acc[bb][jt] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
+  // Dequant constants held in VGPRs, so that mask-and-or is one v_and_or_b32.
+  uint32_t kMask, kMaskHi, kMagic;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
+  asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
+  const uint32_t ssh = 16u * (uint32_t)b;  // the lane's scale: half b of scale word jt
   auto compute = [&](const DenseFrag<BB, GROUPED>& f) {
 #pragma unroll
     for (int jt = 0; jt < 4; jt++) {
-      // column 16 jt + rho: byte b of words rq0 (k 4(h&1) + 0, 1 | 8 + ...) and rq0 + 1
+      // column 16 jt + rho: byte b of words rq0 (k 4(h&1) + 0, 1 | 8 + ...) and rq0 + 1;
+      // magic-exponent conversion as in dequant4 ({k, k+1 | k+8, k+9} of each word)
       const uint32_t x0 = f.w0[jt] >> sh, x1 = f.w1[jt] >> sh;
-      const half4_t d0 = dequant4(x0);  // {k, k+1 | k+8, k+9} of rq0
-      const half4_t d1 = dequant4(x1);  // the same of rq0 + 1
-      half8_t aop = (half8_t){d0.x, d0.y, d1.x, d1.y, d0.z, d0.w, d1.z, d1.w};
+      const half2_t kz = {(_Float16)1032.0f, (_Float16)1032.0f};
+      const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+      const half2_t kzh = {(_Float16)-72.0f, (_Float16)-72.0f};
+      const half2_t l0 = __builtin_bit_cast(half2_t, (x0 & kMask) | kMagic) - kz;
+      const half2_t l1 = __builtin_bit_cast(half2_t, (x1 & kMask) | kMagic) - kz;
+      const half2_t u0 = __builtin_bit_cast(half2_t, (x0 & kMaskHi) | kMagic) * k16 + kzh;
+      const half2_t u1 = __builtin_bit_cast(half2_t, (x1 & kMaskHi) | kMagic) * k16 + kzh;
+      half8_t aop = (half8_t){l0.x, l0.y, l1.x, l1.y, u0.x, u0.y, u1.x, u1.y};
       if constexpr (GROUPED) {
-        const _Float16 sc = f.sc[2 * jt + b];
+        // scale slot 2 jt + b: one shift of word jt (a variable element index would
+        // compile to a select over all eight halves)
+        const uint32_t sw = __builtin_bit_cast(u32x4, f.sc)[jt] >> ssh;
+        const _Float16 sc = __builtin_bit_cast(half2_t, sw).x;
         aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
       }
 #pragma unroll
