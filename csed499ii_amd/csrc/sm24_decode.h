@@ -269,6 +269,11 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const uint32_t nsh = 8u * blk;                     // byte shift: column half in a value word
   // metadata unit bytes -> index halfword: [byte h&1 of int16 blk, of int16 2 + blk]
   const uint32_t msel = (uint32_t)(2 * blk + (h & 1)) | ((uint32_t)(4 + 2 * blk + (h & 1)) << 8) | 0x0c0c0000u;
+  // 3-bit metadata: alignbit shifts of the lane's code word (jb = 0 / 1 half), bit
+  // position of its two codes, and its half's nibble table as 8 bytes
+  const uint32_t m3sh0 = jb ? 24u : 0u, m3sh1 = jb ? 8u : 16u;
+  const uint32_t m3pos = 3u * (4u * blk + 2u * (h & 1));
+  const uint32_t m3tlo = jb ? kTabLowLo : kTabHighLo, m3thi = jb ? kTabLowHi : kTabHighHi;
   const int arow = rho & (MB - 1);                   // staged activation row (lanes rho < MB)
   // direct activation operands: batch rows rho + 16 rb (rows past M repeat row M-1)
   const _Float16* abase[RB];
@@ -440,9 +445,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
           // (jb = 0) or high 24 bits of field "first" (g < 4) or "second" (g >= 4)
-          // at position P = u mod 16, built from words (which, which+1).
+          // at position P = u mod 16, built from words (which, which+1) by one
+          // alignbit.  The lane's two codes of each ehalf (bits pos .. pos + 5) go to
+          // selector bytes of one v_perm over the 8-byte nibble table of its half
+          // (jb), which returns the four index nibbles as bytes; byte pairs are then
+          // folded into the index halfword.
           const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + 2 * q2 * (MPK * 16));
-          idx = 0;
+          uint32_t sel = 0x00000000u;
 #pragma unroll
           for (int ehalf = 0; ehalf < 2; ehalf++) {
             uint32_t X, Y;
@@ -458,14 +467,16 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
               X = mrow[pl];
               Y = mrow[TC / 2 + pl];
             }
-            uint32_t c24;
-            if (which == 0) c24 = jb ? ((X >> 24) | ((Y & 0xFFFFu) << 8)) : (X & 0xFFFFFFu);
-            else c24 = jb ? ((Y >> 8) & 0xFFFFFFu) : (((X >> 16) | (Y << 16)) & 0xFFFFFFu);
-            const uint32_t lut = jb ? kLutLow : kLutHigh;
-            const uint32_t pos = 3u * (4u * blk + 2u * (h & 1));  // nibbles 2(h&1), +1 of int16 blk
-            const uint32_t ca = (c24 >> pos) & 7u, cbv = (c24 >> (pos + 3u)) & 7u;
-            idx |= (((lut >> (4u * ca)) & 15u) | (((lut >> (4u * cbv)) & 15u) << 4)) << (8 * ehalf);
+            // which 0: X (jb 0) or X >> 24 | Y << 8 (jb 1); which 1: X >> 16 | Y << 16
+            // (jb 0) or Y >> 8 (jb 1); bits above 23 are never read
+            const uint32_t c24 = which == 0 ? __builtin_amdgcn_alignbit(Y, X, m3sh0)
+                                            : __builtin_amdgcn_alignbit(Y, jb ? Y : X, m3sh1);
+            const uint32_t ca = (c24 >> m3pos) & 7u, cbv = (c24 >> (m3pos + 3u)) & 7u;
+            sel |= (ca | (cbv << 8)) << (16 * ehalf);
           }
+          const uint32_t nib = __builtin_amdgcn_perm(m3thi, m3tlo, sel);  // bytes: 4 nibbles
+          const uint32_t fold = nib | (nib >> 4);                         // bytes 0, 2: index bytes
+          idx = __builtin_amdgcn_perm(fold, fold, 0x0c0c0200u);
         }
         if constexpr (GROUPED) {
           const _Float16 sc = HOIST ? sr[cb] : *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);

@@ -99,6 +99,15 @@ constexpr int kDecHigh[8] = {14, 13, 8, 13, 3, 4, 9, 12};
 constexpr int kDecLow[8] = {12, 13, 14, 10, 8, 9, 4, 0};
 constexpr uint32_t kLutHigh = lut_of(kDecHigh);
 constexpr uint32_t kLutLow = lut_of(kDecLow);
+// The same tables as bytes (entry c in byte c of the 8-byte pair lo | hi << 32), for
+// a v_perm lookup of up to four codes at once.
+constexpr uint32_t tab_of(const int (&t)[8], int half) {
+  uint32_t v = 0;
+  for (int i = 0; i < 4; i++) v |= (uint32_t)t[4 * half + i] << (8 * i);
+  return v;
+}
+constexpr uint32_t kTabHighLo = tab_of(kDecHigh, 0), kTabHighHi = tab_of(kDecHigh, 1);
+constexpr uint32_t kTabLowLo = tab_of(kDecLow, 0), kTabLowHi = tab_of(kDecLow, 1);
 
 struct GemmArgs {
   const _Float16* A;
