@@ -269,10 +269,11 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const uint32_t nsh = 8u * blk;                     // byte shift: column half in a value word
   // metadata unit bytes -> index halfword: [byte h&1 of int16 blk, of int16 2 + blk]
   const uint32_t msel = (uint32_t)(2 * blk + (h & 1)) | ((uint32_t)(4 + 2 * blk + (h & 1)) << 8) | 0x0c0c0000u;
-  // 3-bit metadata: alignbit shifts of the lane's code word (jb = 0 / 1 half), bit
-  // position of its two codes, and its half's nibble table as 8 bytes
-  const uint32_t m3sh0 = jb ? 24u : 0u, m3sh1 = jb ? 8u : 16u;
+  // 3-bit metadata: bit position of the lane's two codes in its code word, the
+  // 64-bit shifts that bring them to bit 0 (code word of field "first" / "second",
+  // jb = 0 / 1 half), and its half's nibble table as 8 bytes
   const uint32_t m3pos = 3u * (4u * blk + 2u * (h & 1));
+  const uint32_t m3s0 = (jb ? 24u : 0u) + m3pos, m3s1 = (jb ? 40u : 16u) + m3pos;
   const uint32_t m3tlo = jb ? kTabLowLo : kTabHighLo, m3thi = jb ? kTabLowHi : kTabHighHi;
   const int arow = rho & (MB - 1);                   // staged activation row (lanes rho < MB)
   // direct activation operands: batch rows rho + 16 rb (rows past M repeat row M-1)
@@ -445,35 +446,35 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
           // (jb = 0) or high 24 bits of field "first" (g < 4) or "second" (g >= 4)
-          // at position P = u mod 16, built from words (which, which+1) by one
-          // alignbit.  The lane's two codes of each ehalf (bits pos .. pos + 5) go to
-          // selector bytes of one v_perm over the 8-byte nibble table of its half
-          // (jb), which returns the four index nibbles as bytes; byte pairs are then
-          // folded into the index halfword.
+          // at position P = u mod 16, in words (which, which+1).  The lane's two codes
+          // of each ehalf go to selector bytes of one v_perm over the 8-byte nibble
+          // table of its half (jb), which returns the four index nibbles as bytes;
+          // byte pairs are then folded into the index halfword.
           const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + 2 * q2 * (MPK * 16));
-          uint32_t sel = 0x00000000u;
+          uint32_t v[2];
 #pragma unroll
           for (int ehalf = 0; ehalf < 2; ehalf++) {
-            uint32_t X, Y;
-            int which;
+            int which, ix, iy;  // words X = mrow[ix], Y = mrow[iy]
             if constexpr (TC == 64) {
               which = gt >> 2;
               const int Pw = (4 * gt + 2 * jj + ehalf) & 15;
-              X = mrow[16 * which + Pw];
-              Y = mrow[16 * (which + 1) + Pw];
+              ix = 16 * which + Pw;
+              iy = ix + 16;
             } else {
               which = g0 >> 2;
-              const int pl = 4 * gt + 2 * jj + ehalf;
-              X = mrow[pl];
-              Y = mrow[TC / 2 + pl];
+              ix = 4 * gt + 2 * jj + ehalf;
+              iy = ix + TC / 2;
             }
-            // which 0: X (jb 0) or X >> 24 | Y << 8 (jb 1); which 1: X >> 16 | Y << 16
-            // (jb 0) or Y >> 8 (jb 1); bits above 23 are never read
-            const uint32_t c24 = which == 0 ? __builtin_amdgcn_alignbit(Y, X, m3sh0)
-                                            : __builtin_amdgcn_alignbit(Y, jb ? Y : X, m3sh1);
-            const uint32_t ca = (c24 >> m3pos) & 7u, cbv = (c24 >> (m3pos + 3u)) & 7u;
-            sel |= (ca | (cbv << 8)) << (16 * ehalf);
+            // the code word is Y:X >> {0, 24} (which 0, jb 0 / 1) or {16, 40} (which
+            // 1), its two codes at pos and pos + 3: one 64-bit shift by the sum (X and
+            // Y loaded as one register pair)
+            const u32x2 xy = {mrow[ix], mrow[iy]};
+            const uint64_t yx = __builtin_bit_cast(uint64_t, xy);
+            v[ehalf] = (uint32_t)(yx >> (which == 0 ? m3s0 : m3s1));
           }
+          // selector bytes {ca, cb} of ehalf 0, then of ehalf 1
+          const uint32_t s2 = (v[0] & 0x3fu) | ((v[1] & 0x3fu) << 16);
+          const uint32_t sel = (s2 & 0x00070007u) | ((s2 & 0x00380038u) << 5);
           const uint32_t nib = __builtin_amdgcn_perm(m3thi, m3tlo, sel);  // bytes: 4 nibbles
           const uint32_t fold = nib | (nib >> 4);                         // bytes 0, 2: index bytes
           idx = __builtin_amdgcn_perm(fold, fold, 0x0c0c0200u);
