@@ -448,8 +448,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           // (jb = 0) or high 24 bits of field "first" (g < 4) or "second" (g >= 4)
           // at position P = u mod 16, in words (which, which+1).  The lane's two codes
           // of each ehalf go to selector bytes of one v_perm over the 8-byte nibble
-          // table of its half (jb), which returns the four index nibbles as bytes;
-          // byte pairs are then folded into the index halfword.
+          // table of its half (jb), which returns the four index nibbles as bytes,
+          // then folded into the index halfword.
           const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + 2 * q2 * (MPK * 16));
           uint32_t v[2];
 #pragma unroll
@@ -466,18 +466,19 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
               iy = ix + TC / 2;
             }
             // the code word is Y:X >> {0, 24} (which 0, jb 0 / 1) or {16, 40} (which
-            // 1), its two codes at pos and pos + 3: one 64-bit shift by the sum (X and
-            // Y loaded as one register pair)
-            const u32x2 xy = {mrow[ix], mrow[iy]};
-            const uint64_t yx = __builtin_bit_cast(uint64_t, xy);
-            v[ehalf] = (uint32_t)(yx >> (which == 0 ? m3s0 : m3s1));
+            // 1), its two codes at pos and pos + 3: Y:X shifted by the sum S, as one
+            // alignbit of Y:X (S < 32) or of Y:Y by S - 32 (only the low 6 bits are
+            // used)
+            const uint32_t S = which == 0 ? m3s0 : m3s1;
+            const uint32_t Y = mrow[iy], L = mrow[S >= 32u ? iy : ix];
+            v[ehalf] = __builtin_amdgcn_alignbit(Y, L, S & 31u);
           }
-          // selector bytes {ca, cb} of ehalf 0, then of ehalf 1
-          const uint32_t s2 = (v[0] & 0x3fu) | ((v[1] & 0x3fu) << 16);
-          const uint32_t sel = (s2 & 0x00070007u) | ((s2 & 0x00380038u) << 5);
-          const uint32_t nib = __builtin_amdgcn_perm(m3thi, m3tlo, sel);  // bytes: 4 nibbles
-          const uint32_t fold = nib | (nib >> 4);                         // bytes 0, 2: index bytes
-          idx = __builtin_amdgcn_perm(fold, fold, 0x0c0c0200u);
+          // selector bytes {ca0, ca1, cb0, cb1} (code a / b of ehalf 0 / 1): the low
+          // bytes of v[0], v[1] side by side, their b codes moved up by 13 bits
+          const uint32_t s2 = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u);
+          const uint32_t sel = (s2 | (s2 << 13)) & 0x07070707u;
+          const uint32_t nib = __builtin_amdgcn_perm(m3thi, m3tlo, sel);  // the four nibbles as bytes
+          idx = (nib & 0x0f0fu) | ((nib >> 12) & 0xf0f0u);                 // byte e: a | b << 4 of ehalf e
         }
         if constexpr (GROUPED) {
           const _Float16 sc = HOIST ? sr[cb] : *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
