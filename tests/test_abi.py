@@ -97,8 +97,8 @@ def test_plan_without_gpu(built_lib):
     assert p["workgroups"] * (p["threads"] // 64) > 0
     p = marlin.plan_2_4(16, 4096, 22016, sms=256)  # 344 tiles: the 88 past one per CU split in two
     assert p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
-    p = marlin.plan_2_4(24, 4096, 22016)  # wide N above 16 rows: 64-column tiles split in two
-    assert p["kernel"] == "decode" and p["splits"] == 2 and p["workgroups"] == 22016 // 64 * 2
+    p = marlin.plan_2_4(24, 4096, 22016, sms=256)  # wide N above 16 rows: the 88 tail tiles split in two
+    assert p["kernel"] == "decode" and p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
     assert marlin.plan_2_4(24, 4096, 22016, noalloc=True)["splits"] == 1
     assert marlin.plan_2_4(4, 8192, 8192)["splits"] == 1  # 16-column tiles fill the CUs
     assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4  # long K, wider N: K split four ways
