@@ -295,8 +295,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const uint32_t o_act = AOFF + arow * 64 + 16 * au;
   // Dequant constants held in VGPRs, so that mask-and-or is one v_and_or_b32.
   uint32_t kMask, kMaskHi, kMagic;
-  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
-  asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
+  if constexpr (VF == VAL4) {
+    asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(kMask));
+    asm volatile("v_mov_b32 %0, 0x00f000f0" : "=v"(kMaskHi));
+  } else {  // 3-bit codes at bits 0 / 16 and 3 / 19 of a half pair
+    asm volatile("v_mov_b32 %0, 0x00070007" : "=v"(kMask));
+    asm volatile("v_mov_b32 %0, 0x00380038" : "=v"(kMaskHi));
+  }
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
 
   // direct load q = rb * KPW + (k-block of the wave's share)
@@ -409,27 +414,31 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         } else {
           // 3-bit codes: word w is the 24-bit field at byte 3w of the row, nibble p at
           // bits 3p.  Shifted by 6 blk, the lane's four codes (nibbles 2blk, 2blk+1,
-          // 4+2blk, 5+2blk) sit at bits 0, 3, 12, 15 and go straight to the nibble
-          // positions 0, 4 (lo) and 16, 20 (hi) of the 4-bit path.
+          // 4+2blk, 5+2blk) sit at bits 0, 3, 12, 15.
           const uint8_t* rowp = st + o_val + 2 * q2 * (BPK * 16);
           const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
           const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
           const uint32_t y0 = __builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3) + 6 * blk);
           const uint32_t y1 = __builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3) + 6 * blk);
-          // One 24-bit multiply moves both codes of a half pair at once: the masked
-          // fields (bits 0-2 and 12-14; 3-5 and 15-17) times 1 + 2^4 (2^1 + 2^5) land
-          // at bits 0-2 and 16-18 (4-6 and 20-22), and the other copies of the
-          // product fall outside the mask, with no carries between them.
-          lo0 = (__umul24(y0 & 0x7007u, 17u) & 0x00070007u) | kMagic;
-          lo1 = (__umul24(y1 & 0x7007u, 17u) & 0x00070007u) | kMagic;
-          hi0 = (__umul24(y0 & 0x38038u, 34u) & 0x00700070u) | kMagic;
-          hi1 = (__umul24(y1 & 0x38038u, 34u) & 0x00700070u) | kMagic;
+          // One shift and one bit-field insert move the codes at bits 12 and 15 up to
+          // 16 and 19, so that each half pair's codes sit 16 bits apart: masked and
+          // or-ed with the magic exponent they are the halves 1024 + c (bits 0 / 16)
+          // and 1024 + 8c (bits 3 / 19), both exact.
+          const uint32_t z0 = (y0 & 0x0000FFFFu) | ((y0 << 4) & 0xFFFF0000u);
+          const uint32_t z1 = (y1 & 0x0000FFFFu) | ((y1 << 4) & 0xFFFF0000u);
+          lo0 = (z0 & kMask) | kMagic;
+          lo1 = (z1 & kMask) | kMagic;
+          hi0 = (z0 & kMaskHi) | kMagic;
+          hi1 = (z1 & kMaskHi) | kMagic;
         }
         constexpr float zp = VF == VAL4 ? 1032.0f : 1028.0f;  // 1024 + zero point
-        constexpr float zh = (zp - 1024.0f) + 64.0f;          // the same for 1024 + 16 q, over 16
+        // the high pair is 1024 + 16 q (4-bit) or 1024 + 8 q (3-bit): times 1/16 (1/8)
+        // less 64 (128) and the zero point, exact
+        constexpr float hs = VF == VAL4 ? 0.0625f : 0.125f;
+        constexpr float zh = (zp - 1024.0f) + 1024.0f * hs;
         const half2_t kz = {(_Float16)zp, (_Float16)zp};
-        const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const half2_t k16 = {(_Float16)hs, (_Float16)hs};
         const half2_t kzh = {(_Float16)-zh, (_Float16)-zh};
         const half2_t l0 = __builtin_bit_cast(half2_t, lo0) - kz;
         const half2_t l1 = __builtin_bit_cast(half2_t, lo1) - kz;
