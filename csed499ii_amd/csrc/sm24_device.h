@@ -129,8 +129,9 @@ constexpr int kDecodeMaxM = 32;       // largest batch of one decode launch (two
 constexpr int kDecodeChunkMaxM = 96;  // largest batch run as several decode launches
 constexpr int kPreTileCols = 512;
 constexpr int kPreThreads = 512;  // one wave per 64-column chunk of the tile
-constexpr size_t kPreSplitBytes = 512 * 128 * sizeof(float);  // fp32 partial of one tile
-hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream);
+// fp32 partial of one tile of `rows` (128 or 64) batch rows
+constexpr size_t pre_split_bytes(int rows) { return (size_t)512 * rows * sizeof(float); }
+hipError_t launch_prefill(const GemmArgs& a, int rows, bool grouped, hipStream_t stream);
 
 template <int ABID>
 __device__ __forceinline__ float4_t smfmac32(half4_t a, half8_t b, float4_t c, uint32_t idx) {
@@ -156,6 +157,14 @@ __device__ __forceinline__ void dma16x2(uint32_t lds, const uint32_t (&v)[2], co
       "global_load_lds_dwordx4 %1, %3\n\t"
       "global_load_lds_dwordx4 %2, %3 offset:1024" ::"s"(lds),
       "v"(v[0]), "v"(v[1]), "s"(base)
+      : "memory", "m0");
+}
+// As dma16x2 with one instruction: 16 bytes per lane from base + v into lds + 16 lane.
+__device__ __forceinline__ void dma16x1(uint32_t lds, uint32_t v, const void* base) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2" ::"s"(lds),
+      "v"(v), "s"(base)
       : "memory", "m0");
 }
 // One wave's weight side of a k-step, into lds + [0, 1792): 16 bytes per lane from

@@ -448,34 +448,68 @@ __global__ __launch_bounds__(256) void w3_to_w4_kernel(const uint32_t* __restric
   out[i] = o;
 }
 
-// K splits of the large-M kernel.  Its workgroups fill the CUs one per CU, so a
-// problem with few tiles runs faster split along K when K is long enough to pay for
-// the hand-off: each split stores a 256 KiB fp32 partial to uncached scratch and the
-// last one reads them all back.  The estimate is rounds x (k-steps per split) plus
-// that traffic, at the rates measured on MI355X (0.67 us per k-step of a tile, ~2.5
-// TB/s for the exchange: forced splits 2-4 on the Llama-2-7B and -70B shapes at M =
-// 128..1024).  MARLIN_HIP_PREFILL_SPLITS forces a count (read once).
-int prefill_splits(int tiles, int nks, int cus) {
+// Tile height and K splits of the large-M kernel.  Its workgroups run one per CU, and
+// the chip is power-limited at full occupancy: a 128-row k-step takes ~0.61 us with 64
+// workgroups busy and ~1.03 us with all 256 CUs busy (MI355X, Llama-2-70B prefill
+// shapes).  So a problem with few tiles runs on 64-row tiles (twice the tiles, each
+// k-step 0.63 of a 128-row one at the same occupancy: half the MFMAs at twice the
+// dequantization per MFMA) or split along K when K is long enough to pay for the
+// hand-off: each split stores its fp32 partial (512 x rows floats) to uncached scratch
+// and the last one reads them all back, ~5 TB/s for that exchange.  The estimate sums
+// the rounds of workgroups over the CUs, each at the k-step time of its occupancy,
+// plus the exchange; it reproduces the measured times of every prefill-sweep call to
+// within ~5 % for both heights and 1-2 splits (forced by MARLIN_HIP_PREFILL_ROWS and
+// MARLIN_HIP_PREFILL_SPLITS, read once).  `nosplit`: one split only.
+int env_choice(const char* name, std::initializer_list<int> allowed, int fallback);
+struct PrefillPlan {
+  int rows;    // batch rows per tile: 128 or 64
+  int splits;  // K splits
+  int tiles;   // tiles (workgroups per split)
+};
+// k-step time (us) of a 128-row tile with a fraction x of the CUs busy (measured).
+double prefill_step_us(double x) {
+  static const double xs[] = {0.0, 0.25, 0.3125, 0.5, 0.625, 1.0};
+  static const double us[] = {0.55, 0.61, 0.62, 0.70, 0.78, 1.03};
+  if (x >= 1.0) return us[5];
+  int i = 0;
+  while (x > xs[i + 1]) i++;
+  return us[i] + (us[i + 1] - us[i]) * (x - xs[i]) / (xs[i + 1] - xs[i]);
+}
+PrefillPlan prefill_plan(int M, int N, int K, int cus, bool nosplit) {
   static const int forced = [] {
     const char* e = getenv("MARLIN_HIP_PREFILL_SPLITS");
     const int x = e ? atoi(e) : 0;
     return x >= 1 && x <= 16 ? x : 0;
   }();
-  const int max_s = nks / 8;  // at least eight k-steps per split
-  if (forced) return forced < max_s ? forced : (max_s > 0 ? max_s : 1);
-  const double step_us = 0.67, exchange_bytes_per_us = 2.5e6;
-  int best_s = 1;
-  double best = 1e30;
-  for (int s = 1; s <= 8 && s <= max_s; s++) {
-    const long long rounds = ((long long)tiles * s + cus - 1) / cus;
-    const double traffic = s > 1 ? 2.0 * tiles * s * (double)kPreSplitBytes : 0.0;
-    const double cost = (double)rounds * step_us * nks / s + traffic / exchange_bytes_per_us;
-    if (cost < 0.97 * best) {
-      best = cost;
-      best_s = s;
+  static const int forced_rows = env_choice("MARLIN_HIP_PREFILL_ROWS", {64, 128}, 0);
+  const int nks = K / 64;
+  const int max_s = nosplit ? 1 : (nks / 8 > 0 ? nks / 8 : 1);  // at least eight k-steps per split
+  if (cus < 1) cus = 1;
+  const double exchange_bytes_per_us = 5.0e6;
+  PrefillPlan best{128, 1, (N / kPreTileCols) * ((M + 127) / 128)};
+  double best_cost = 1e30;
+  for (int rows = 128; rows >= 64; rows -= 64) {
+    if (forced_rows && rows != forced_rows) continue;
+    const int tiles = (N / kPreTileCols) * ((M + rows - 1) / rows);
+    if (forced && !nosplit) return PrefillPlan{rows, forced < max_s ? forced : max_s, tiles};
+    const double hscale = rows == 128 ? 1.0 : 0.63;
+    for (int s = 1; s <= 8 && s <= max_s; s++) {
+      const long long wgs = (long long)tiles * s, full = wgs / cus, tail = wgs - full * cus;
+      double cost = ((double)full * prefill_step_us(1.0) + (tail ? prefill_step_us((double)tail / cus) : 0.0)) *
+                    hscale * nks / s;
+      if (s > 1) cost += 2.0 * tiles * s * (double)pre_split_bytes(rows) / exchange_bytes_per_us;
+      if (cost < 0.98 * best_cost) {
+        best_cost = cost;
+        best = PrefillPlan{rows, s, tiles};
+      }
     }
   }
-  return best_s;
+  return best;
+}
+
+// A split plan needs one arrival counter per tile (at most 64-row tiles: the most).
+bool prefill_counters_exceed(int N, int M) {
+  return (size_t)(N / kPreTileCols) * ((M + 63) / 64) * sizeof(uint32_t) > kCounterBytes;
 }
 
 struct Plan {
@@ -835,12 +869,10 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
     out[3] = d.splits;
     out[4] = (M + kDecodeMaxM - 1) / kDecodeMaxM;
   } else if (kernel == KERNEL_PREFILL) {
-    const int tiles = (N / kPreTileCols) * ((M + 127) / 128);
-    int splits = noalloc ? 1 : prefill_splits(tiles, K / 64, sms);
-    if (splits > 1 && (size_t)tiles * sizeof(uint32_t) > kCounterBytes) splits = 1;
-    out[1] = tiles * splits;
+    const PrefillPlan pp = prefill_plan(M, N, K, sms, noalloc || prefill_counters_exceed(N, M));
+    out[1] = pp.tiles * pp.splits;
     out[2] = kPreThreads;
-    out[3] = splits;
+    out[3] = pp.splits;
     out[4] = 1;
   } else {
     Plan plan = plan_for(M, N, K, sms);
@@ -951,15 +983,18 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
     p.M = M;
     p.N = N;
     p.K = K;
-    const int tiles = (N / kPreTileCols) * ((M + 127) / 128);
-    p.splits = noalloc ? 1 : prefill_splits(tiles, K / 64, sms);
-    if (p.splits > 1 && (size_t)tiles * sizeof(uint32_t) > kCounterBytes) p.splits = 1;
+    PrefillPlan pp = prefill_plan(M, N, K, sms, noalloc || prefill_counters_exceed(N, M));
+    p.splits = pp.splits;
     if (p.splits > 1) {
-      err = get_scratch(dev, stream, (size_t)tiles * p.splits * kPreSplitBytes, &p.counters, &p.partial);
+      err = get_scratch(dev, stream, (size_t)pp.tiles * p.splits * pre_split_bytes(pp.rows), &p.counters,
+                        &p.partial);
       if (err != MARLIN_HIP_OK) return err;
-      if (!p.counters) p.splits = 1;
+      if (!p.counters) {  // no scratch: the best unsplit plan
+        pp = prefill_plan(M, N, K, sms, true);
+        p.splits = 1;
+      }
     }
-    return launch_error(launch_prefill(p, groupsize != -1, stream));
+    return launch_error(launch_prefill(p, pp.rows, groupsize != -1, stream));
   }
   Plan plan = plan_for(M, N, K, sms);
   const int chunks = N / 64;

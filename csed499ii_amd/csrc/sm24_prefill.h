@@ -44,11 +44,9 @@ struct IntC {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kPreRows = 128;  // batch rows per tile
 constexpr int kPreChunks = 8;  // 64-column chunks per tile = waves per workgroup
 static_assert(64 * kPreChunks == kPreTileCols && kPreThreads == 64 * kPreChunks, "tile width");
 constexpr int kPreRing = 4;                        // k-steps resident in LDS
-constexpr int kPreActB = kPreRows * 128;           // activation bytes of one k-step
 // Weight side of one k-step, per wave (one chunk): packed values of both k-blocks
 // (1 KiB), metadata of both k-blocks (2 x 256 B), scales of the chunk pair (256 B),
 // contiguous so that one M0 value serves the wave's weight-side DMAs (instruction
@@ -56,10 +54,16 @@ constexpr int kPreActB = kPreRows * 128;           // activation bytes of one k-
 constexpr int kPreWgtW = 1792;
 constexpr int kPreWgtB = kPreChunks * kPreWgtW;    // weight side of one k-step
 constexpr int kPreActOff = 0;
-constexpr int kPreWgtOff = kPreActOff + kPreRing * kPreActB;
-constexpr int kPreLdsBytes = kPreWgtOff + kPreRing * kPreWgtB;
+// LDS layout of a tile of RG 32-row blocks (128 or 64 batch rows): the activation
+// ring (32 RG rows x 128 bytes per k-step), then the weight ring.
+template <int RG>
+struct PreLds {
+  static constexpr int act_b = 32 * RG * 128;  // activation bytes of one k-step
+  static constexpr int wgt_off = kPreActOff + kPreRing * act_b;
+  static constexpr int bytes = wgt_off + kPreRing * kPreWgtB;
+};
 static_assert(kPreWgtW % 256 == 0, "wave blocks keep the bank pattern");
-static_assert(kPreLdsBytes <= 160 * 1024, "LDS");
+static_assert(PreLds<4>::bytes <= 160 * 1024, "LDS");
 
 // v_smfmac_f32_32x32x32_f16 with the accumulator in AGPRs; ABID selects the index
 // halfword.  Written as inline assembly because, for the intrinsic, the compiler
@@ -87,11 +91,29 @@ __device__ __forceinline__ void pre_step_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(NDMA) : "memory");
 }
 
-template <bool GROUPED>
+// First dequantization slice of MFMA region r of a k-step with nr regions: the 14
+// slices of the next step's two k-blocks run in regions 2..nr-1, one per region with
+// 16 regions, with 8 three or two per region (k-block 0 in regions 2-4, 1 in 5-7).
+constexpr int pre_slice0(int nr, int r) {
+  return r <= 2 ? 0 : nr == 16 ? r - 2 : r == 3 ? 3 : r == 4 ? 5 : r == 5 ? 7 : r == 6 ? 10 : r == 7 ? 12 : 14;
+}
+static_assert(pre_slice0(16, 16) == 14 && pre_slice0(8, 8) == 14, "every slice once");
+
+// RG: 32-row B fragments per wave, i.e. a tile of 32 RG batch rows.  RG = 4 is the
+// tile described above; RG = 2 (64 rows) doubles the tiles of a call for batches whose
+// 128-row tiles leave CUs idle, at twice the dequantization per MFMA (each weight
+// fragment feeds two B fragments instead of four: ~6.5 VALU per MFMA).
+template <bool GROUPED, int RG>
 __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a) {
-  constexpr int MT = kPreRows, CT = kPreChunks;
-  constexpr int NDMA = GROUPED ? 6 : 5;  // DMA instructions per wave and k-step
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kPreLdsBytes];
+  static_assert(RG == 4 || RG == 2, "128- or 64-row tiles");
+  constexpr int MT = 32 * RG, CT = kPreChunks;
+  constexpr int NF = 2 * RG;               // B fragments per k-step (two k-blocks)
+  constexpr int NR = 2 * NF;               // MFMA regions per k-step
+  constexpr int ADMA = RG / 2;             // activation DMA instructions per wave and k-step
+  constexpr int NDMA = ADMA + (GROUPED ? 4 : 3);  // DMA instructions per wave and k-step
+  constexpr int kPreActB = PreLds<RG>::act_b, kPreWgtOff = PreLds<RG>::wgt_off;
+  constexpr int PSTRIDE = 16384 * RG;      // floats of one (tile, split) partial
+  __shared__ __attribute__((aligned(16))) uint8_t lds[PreLds<RG>::bytes];
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const uint32_t lbase = (uint32_t)(size_t)(lds_u8*)lds;
 
@@ -133,14 +155,14 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   const int cw = c0 + w;          // chunk of this wave
 
   // ---- DMA sources: per-lane byte offsets from per-k-step bases ----
-  // activations: instruction u of wave w fills pieces 64(2w + u) + lane of the step's
-  // 1024 16-byte pieces; piece P = row P >> 3, physical slot P & 7, which holds the
-  // logical slot (P & 7) ^ ((row >> 1) & 7).  Rows past M repeat row M-1 (never
-  // stored); the host keeps 2 M K + 4096 below 2^32.
-  uint32_t act_v[2];
+  // activations: instruction u of wave w fills pieces 64(ADMA w + u) + lane of the
+  // step's 256 RG 16-byte pieces; piece P = row P >> 3, physical slot P & 7, which
+  // holds the logical slot (P & 7) ^ ((row >> 1) & 7).  Rows past M repeat row M-1
+  // (never stored); the host keeps 2 M K + 4096 below 2^32.
+  uint32_t act_v[ADMA];
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
-    const int p = 64 * (2 * w + u) + lane, row = p >> 3;
+  for (int u = 0; u < ADMA; u++) {
+    const int p = 64 * (ADMA * w + u) + lane, row = p >> 3;
     const int ls = (p & 7) ^ ((row >> 1) & 7);
     const int m = m0 + row < M ? m0 + row : M - 1;
     // + 1024 (1 - u): instruction u carries offset 1024 u, the base is lowered by 1024
@@ -167,14 +189,15 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   const uint32_t strB = 16 * (uint32_t)N, strM = 8 * (uint32_t)N, strS = 2 * (uint32_t)N;
 
   // DMA group g of local k-step s (clamped to the split's last) into ring slot q:
-  // g = 0 this wave's share of the step's activation rows (2 instructions), g = 1 the
+  // g = 0 this wave's share of the step's activation rows (ADMA instructions), g = 1 the
   // weight side of its chunk (packed values, metadata of both k-blocks, and the
   // scales of its chunk pair when grouped).  Step offsets are 32-bit: the host keeps
   // K N / 4 below 2^32.
   auto dma = [&](int s, int q, int g) {
     const uint32_t sc = (uint32_t)(ks0 + s < ks1 ? ks0 + s : ks1 - 1);
     if (g == 0) {
-      dma16x2(lbase + kPreActOff + q * kPreActB + 2048 * w, act_v, gA1 + 128 * sc);
+      if constexpr (ADMA == 2) dma16x2(lbase + kPreActOff + q * kPreActB + 2048 * w, act_v, gA1 + 128 * sc);
+      else dma16x1(lbase + kPreActOff + q * kPreActB + 1024 * w, act_v[0], gA1 + 128 * sc);
     } else {
       const uint32_t l = lbase + kPreWgtOff + q * kPreWgtB + kPreWgtW * w;
       if constexpr (GROUPED)
@@ -212,10 +235,10 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
 
   half8_t av[2][2][2];  // [parity][kb][hf] dequantized weight fragments
   uint32_t ix[2][2];    // [parity][kb] index halfwords (hf = abid)
-  half16_t bv[4];       // B fragments, ring by fragment number kb*4 + rg
-  f32x16 acc[4][2];     // [rg][hf]
+  half16_t bv[4];       // B fragments, ring by fragment number kb*RG + rg
+  f32x16 acc[RG][2];    // [rg][hf]
 #pragma unroll
-  for (int rg = 0; rg < 4; rg++)
+  for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) {
       acc[rg][hf] = (f32x16){};
@@ -223,7 +246,7 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
     }
 
   auto read_b = [&](int q, int f) -> half16_t {
-    const int kb = f >> 2, rg = f & 3;
+    const int kb = f / RG, rg = f % RG;
     const uint8_t* p0 = lds + b_off[kb][0] + q * kPreActB + rg * 4096;
     const uint8_t* p1 = lds + b_off[kb][1] + q * kPreActB + rg * 4096;
     const half8_t lo = *reinterpret_cast<const half8_t*>(p0);
@@ -314,27 +337,29 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   // ---- k-step s in ring slot Q = s & 3 (slot Q+1: step s+1, slot Q+3: step s+3):
   //   barrier: this wave's DMAs of step s+1 have landed, every wave has finished step
   //   s-1 (its reads of slot Q+3);
-  //   16 regions r = (kb, rg, hf), each one MFMA plus a share of: DMA group r >> 1 of
-  //   step s+3 (r = 1, 3); at hf = 0 the read of B fragment f+3 (f = 4kb + rg; from
-  //   step s+1 past 7; its ring slot held fragment f-1, used up by then); at r < 2 the raw words and metadata of step s+1, k-block r,
-  //   and at r = 2 its scales; at r >= 2 slice (r-2) % 7 of dequantizing k-block
-  //   (r-2) / 7 of step s+1.
+  //   NR = 4 RG regions r = (kb, rg, hf), each one MFMA plus a share of: DMA group
+  //   r >> 1 of step s+3 (r = 1, 3); at hf = 0 the read of B fragment f+3 (f = RG kb +
+  //   rg; from step s+1 past NF-1; its ring slot held fragment f-1, used up by then);
+  //   at r < 2 the raw words and metadata of step s+1, k-block r, and at r = 2 its
+  //   scales; at r >= 2 the slices [pre_slice0(r), pre_slice0(r+1)) of dequantizing
+  //   step s+1 (slice i: slice i % 7 of k-block i / 7).
   // Steps past the last are skipped (uniform); the DMAs are clamped, so the vmcnt of
   // every barrier counts exactly the DMAs of one step. ----
   auto step = [&](int s, auto qc) {
     constexpr int Q = decltype(qc)::value, P = Q & 1, QN = (Q + 1) & 3, QD = (Q + 3) & 3;
     pre_step_barrier<NDMA>();
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int kb = r >> 3, rg = (r >> 1) & 3, hf = r & 1, f = r >> 1;
+    for (int r = 0; r < NR; r++) {
+      const int kb = r / (2 * RG), rg = (r >> 1) % RG, hf = r & 1, f = r >> 1;
       if (hf) pre_smfmac<1>(acc[rg][hf], av[P][kb][hf], bv[f & 3], ix[P][kb]);
       else pre_smfmac<0>(acc[rg][hf], av[P][kb][hf], bv[f & 3], ix[P][kb]);
       __builtin_amdgcn_sched_barrier(0);  // the region's work follows its MFMA
-      if (hf == 0) bv[(f + 3) & 3] = read_b(f + 3 < 8 ? Q : QN, (f + 3) & 7);
+      if (hf == 0) bv[(f + 3) & 3] = read_b(f + 3 < NF ? Q : QN, (f + 3) % NF);
       if (r == 1 || r == 3) dma(s + 3, QD, r >> 1);
       if (r < 2) read_raw(QN, r);
       if (r == 2) read_scales(QN);
-      if (r >= 2) dq_slice((r - 2) / 7, (r - 2) % 7, P ^ 1);
+#pragma unroll
+      for (int i = pre_slice0(NR, r); i < pre_slice0(NR, r + 1); i++) dq_slice(i / 7, i % 7, P ^ 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -371,21 +396,21 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   pre_mfma_drain();
 #pragma unroll
-  for (int rg = 0; rg < 4; rg++)
+  for (int rg = 0; rg < RG; rg++)
 #pragma unroll
     for (int hf = 0; hf < 2; hf++) asm volatile("" : "+a"(acc[rg][hf]));
 
   // ---- split-K hand-off: the partial tile goes to uncached scratch in register order
-  // ([tile][split][wave][rg][hf][i][lane] float4s, 256 KiB per tile and split); the
+  // ([tile][split][wave][rg][hf][i][lane] float4s, 64 RG KiB per tile and split); the
   // last split to arrive at the tile's counter reads all splits back and adds them in
   // split order (so the result is bit-identical from run to run, whichever split comes
   // last), writes C and resets the counter.  Each thread's stores complete before the
   // workgroup barrier; the counter is bumped after it. ----
-  const float* const pbase = a.partial + ((size_t)tile * S) * 65536 + (size_t)w * 8192 + 4 * lane;
+  const float* const pbase = a.partial + ((size_t)tile * S) * PSTRIDE + (size_t)w * (2048 * RG) + 4 * lane;
   if (S > 1) {
-    float* const pmine = a.partial + ((size_t)tile * S + z) * 65536 + (size_t)w * 8192 + 4 * lane;
+    float* const pmine = a.partial + ((size_t)tile * S + z) * PSTRIDE + (size_t)w * (2048 * RG) + 4 * lane;
 #pragma unroll
-    for (int rg = 0; rg < 4; rg++) {
+    for (int rg = 0; rg < RG; rg++) {
       if (m0 + 32 * rg >= M) break;  // 32-row blocks past M are never read back (uniform)
 #pragma unroll
       for (int hf = 0; hf < 2; hf++)
@@ -410,7 +435,7 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   // from every split, in split order, two splits' 8 float4s per batch of loads: the
   // uncached reads are latency-bound, so each batch keeps 16 loads in flight. ----
 #pragma unroll
-  for (int rg = 0; rg < 4; rg++) {
+  for (int rg = 0; rg < RG; rg++) {
     if (m0 + 32 * rg >= M) break;  // uniform: no rows of this block are stored
     float4_t v[2][4];
     if (S == 1) {
@@ -428,11 +453,11 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
         const bool two = zz + 1 < S;  // uniform
         float4_t t0[8], t1[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) t0[k] = *reinterpret_cast<const float4_t*>(p + k * 256 + (size_t)zz * 65536);
+        for (int k = 0; k < 8; k++) t0[k] = *reinterpret_cast<const float4_t*>(p + k * 256 + (size_t)zz * PSTRIDE);
         if (two) {
 #pragma unroll
           for (int k = 0; k < 8; k++)
-            t1[k] = *reinterpret_cast<const float4_t*>(p + k * 256 + (size_t)(zz + 1) * 65536);
+            t1[k] = *reinterpret_cast<const float4_t*>(p + k * 256 + (size_t)(zz + 1) * PSTRIDE);
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) v[k >> 2][k & 3] += t0[k];

@@ -3,10 +3,15 @@
 
 namespace sm24 {
 
-hipError_t launch_prefill(const GemmArgs& a, bool grouped, hipStream_t stream) {
-  const int tiles = (a.N / (64 * kPreChunks)) * ((a.M + kPreRows - 1) / kPreRows) * a.splits;
-  if (grouped) hipLaunchKernelGGL(sm24_prefill_kernel<true>, dim3(tiles), dim3(kPreThreads), 0, stream, a);
-  else hipLaunchKernelGGL(sm24_prefill_kernel<false>, dim3(tiles), dim3(kPreThreads), 0, stream, a);
+hipError_t launch_prefill(const GemmArgs& a, int rows, bool grouped, hipStream_t stream) {
+  const dim3 grid((a.N / (64 * kPreChunks)) * ((a.M + rows - 1) / rows) * a.splits);
+  if (rows == 64) {
+    if (grouped) hipLaunchKernelGGL((sm24_prefill_kernel<true, 2>), grid, dim3(kPreThreads), 0, stream, a);
+    else hipLaunchKernelGGL((sm24_prefill_kernel<false, 2>), grid, dim3(kPreThreads), 0, stream, a);
+  } else {
+    if (grouped) hipLaunchKernelGGL((sm24_prefill_kernel<true, 4>), grid, dim3(kPreThreads), 0, stream, a);
+    else hipLaunchKernelGGL((sm24_prefill_kernel<false, 4>), grid, dim3(kPreThreads), 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -108,8 +108,13 @@ def test_plan_without_gpu(built_lib):
         p = marlin.plan_2_4(M, 8192, 57344)
         assert p["kernel"] == "large_m" and p["threads"] == 512
         assert p["workgroups"] == 57344 // 512 * (M // 128) * p["splits"]
-    assert marlin.plan_2_4(512, 8192, 10240)["splits"] > 1  # few tiles: split K
-    assert marlin.plan_2_4(512, 8192, 10240, noalloc=True)["splits"] == 1
+    # few tiles: 64-row tiles (qkv: 160 of them), and split K (o: two ways)
+    p = marlin.plan_2_4(512, 8192, 10240, sms=256)
+    assert p["kernel"] == "large_m" and p["splits"] == 1 and p["workgroups"] == 10240 // 512 * (512 // 64)
+    p = marlin.plan_2_4(512, 8192, 8192, sms=256)
+    assert p["splits"] == 2 and p["workgroups"] == 2 * 8192 // 512 * (512 // 64)
+    assert marlin.plan_2_4(512, 28672, 8192, sms=256)["splits"] == 4  # long K: 128-row tiles split four ways
+    assert marlin.plan_2_4(512, 8192, 8192, noalloc=True)["splits"] == 1
     assert marlin.plan_2_4(300, 4096, 768)["kernel"] == "general"  # N % 512 != 0
     with pytest.raises(RuntimeError, match="not compatible"):
         marlin.plan_2_4(16, 1000, 512)

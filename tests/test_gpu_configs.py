@@ -28,11 +28,14 @@ def _mul(A, wt, C=None):
     return C
 
 
-# (shape, M), grouped by shape so that each 70B weight is built once.  M = 512 splits
-# K for qkv, o and down; down splits again at M = 1024; gate_up at M = 4096 is the
-# largest grid (3584 workgroups).
+# (shape, M), grouped by shape so that each 70B weight is built once.  The planner's
+# choices (256 CUs): qkv at M = 512 and o at M = 1024 run 64-row tiles unsplit, o at
+# M = 512 64-row tiles split in two; down splits 128-row tiles four ways at M = 512
+# and two ways at M = 1024; o at M = 4000 has a ragged last 128-row tile; gate_up at
+# M = 4096 is the largest grid (3584 workgroups).
 PREFILL_CASES = [(name, M) for name in ("qkv", "o", "down", "gate_up")
-                 for M in ((512, 1024, 4096) if name == "down" else (512, 4096))]
+                 for M in {"qkv": (512, 1024, 4096), "o": (512, 1024, 4000), "down": (512, 1024, 4096),
+                           "gate_up": (512, 4096)}[name]]
 
 
 @pytest.mark.parametrize("name,M", PREFILL_CASES)

@@ -170,7 +170,8 @@ def test_decode_llama70b_full_size_slices(K, N, M):
                                      (80, 16384, 512, 128), (100, 8192, 512, -1), (160, 4096, 512, 128)])
 def test_prefill_kernel_shapes(M, N, K, g):
     """The large-M kernel: ragged row tiles, 1-3 k-steps, per-column and grouped
-    scales, several column tiles (every XCD ordering branch)."""
+    scales, several column tiles (every XCD ordering branch).  Problems this small
+    have few tiles, so the planner gives them 64-row tiles."""
     wt, A = _problem(M, N, K, g, 900 + M + K)
     C = _run(wt, A)
     _check(wt, A, C, f"prefill M={M} N={N} K={K} g={g}")
@@ -180,7 +181,8 @@ def test_prefill_kernel_shapes(M, N, K, g):
 @pytest.mark.parametrize("M,N,K,g", [(300, 512, 8192, -1), (1000, 2048, 8192, 128), (256, 1024, 4096, 128),
                                      (100, 4096, 4096, 128), (130, 4096, 11008, -1)])
 def test_prefill_split_k(M, N, K, g):
-    """Large-M kernel split along K (few tiles, long K: the planner picks 3-7 splits):
+    """Large-M kernel split along K (few tiles, long K: the planner picks 3-8 splits
+    of 64-row tiles):
     partials handed off through the scratch, reduced by the last split in split order,
     so repeated calls agree bit for bit and the counters return to zero."""
     wt, A = _problem(M, N, K, g, 1700 + M + K)

@@ -152,9 +152,10 @@ def test_checker_catches_planted_hazards():
 
 def test_prefill_smfmac_hazards(prefill_asm):
     kernels = _kernels(prefill_asm)
-    assert len(kernels) == 2  # grouped and per-column scales
+    assert len(kernels) == 4  # grouped and per-column scales, 128- and 64-row tiles
     for name, body in kernels.items():
-        assert sum(1 for l in body.split("\n") if "v_smfmac" in l) >= 64, name
+        # four unrolled k-steps of 16 (128 rows) or 8 (64 rows) smfmacs
+        assert sum(1 for l in body.split("\n") if "v_smfmac" in l) >= (32 if "ELi2E" in name else 64), name
         assert hazards(body) == [], name
 
 
@@ -162,9 +163,10 @@ def test_prefill_registers(prefill_asm):
     for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", prefill_asm, re.S):
         body = m.group(2)
         assert int(re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", body).group(1)) == 0, m.group(1)
-    # 128 accumulator registers in AGPRs, and at most 128 VGPRs, so that two waves fit
-    # on a SIMD
+    # 128 (128-row tiles) or 64 (64-row tiles) accumulator registers in AGPRs, and at
+    # most 128 VGPRs, so that two waves fit on a SIMD
     assert prefill_asm.count("; NumAgprs: 128") == 2
+    assert prefill_asm.count("; NumAgprs: 64") == 2
     for v in re.findall(r"; NumVgprs: (\d+)", prefill_asm):
         assert int(v) <= 128
 
