@@ -3,7 +3,9 @@
 // Workgroup tile: 512 output columns (8 chunks of 64) x 128 batch rows, 8 waves, two
 // per SIMD; wave w owns chunk w (64 columns) for all 128 rows as 4 x 2
 // v_smfmac_f32_32x32x32_f16 accumulators (128 AGPRs).  K advances in steps of 64 (two
-// 32-deep k-blocks); one k-step is 16 MFMAs per wave.
+// 32-deep k-blocks); one k-step is 16 MFMAs per wave.  A second instantiation
+// (template argument RG = 2) runs 64-row tiles: 2 x 2 accumulators (64 AGPRs), 8
+// MFMAs per k-step, for calls whose 128-row tiles would leave CUs idle.
 //
 // Why two waves per SIMD.  Measured on MI355X (random operands): a 32x32x32 smfmac
 // takes ~35 cycles, and the VALU can issue ~4 instructions of 4 cycles beside it.
