@@ -794,21 +794,26 @@ hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool 
 
 // Large-M path (sm24_prefill_kernel): 4-bit values and metadata, N a multiple of its
 // 512-column tile and K of its 64-deep k-step, from a batch threshold measured on
-// MI355X (Llama-2-7B shapes, M in 48..384, against decode launches of <= 32 rows and
-// the general kernel).  Below ~128 rows one 128-row tile per 512 columns leaves most
-// CUs idle and the planner splits K, so decode launches win while their count stays
-// small: M >= 65 for N >= 16384 (gate_up at M = 96: 43.8 against 57.9 us), M >= 97
-// for N >= 4096 (qkv at M = 96: 34.3 against 35.6 us; down at M = 96: 43.5 against
-// 35.3; at M = 144 o takes 33.3 against 44.9 us on the general kernel, down 46.4
-// against 80.4), M >= 160 for narrower N.  MARLIN_HIP_PREFILL_MIN_M (> 32) replaces
-// the threshold.
+// MI355X against decode launches of <= 32 rows (Llama-2-7B and -70B shapes, M in
+// 48..192, the planner's 64- or 128-row tiles): from M = 33 for the widest N (7B
+// gate_up 4096x22016 at M = 48 / 64: 23.5 / 23.3 against 28.1 / 34.0 us) and for long
+// K at N >= 10240 (70B qkv 8192x10240: 25.9 / 26.1 against 28.9 / 34.3 us); from
+// M = 65 for N >= 4096 (M = 80 / 96: 7B qkv 23.0 / 22.8 against 28.4 / 31.7 us, 7B down
+// 28.2 / 28.5 against 30.3 / 32.8, 70B o 27.9 / 27.5 against 36.1 / 39.7; at M = 48 /
+// 64 the decode launches win for 7B o, down and qkv: 7B o 13.6 / 15.0 against 19.6 /
+// 20.0 us); M >= 160 for narrower N.  MARLIN_HIP_PREFILL_MIN_M (> 32) replaces the
+// threshold.
+int prefill_min_m(int N, int K) {
+  if (N >= 16384 || (N >= 10240 && K >= 8192)) return kDecodeMaxM + 1;
+  return N >= 4096 ? 65 : 160;
+}
 bool prefill_fits(int M, int N, int K, int vf, int mf) {
   static const int forced_min_m = [] {
     const char* e = getenv("MARLIN_HIP_PREFILL_MIN_M");
     const int x = e ? atoi(e) : 0;
     return x > kDecodeMaxM ? x : 0;
   }();
-  const int min_m = forced_min_m ? forced_min_m : (N >= 16384 ? 65 : (N >= 4096 ? 97 : 160));
+  const int min_m = forced_min_m ? forced_min_m : prefill_min_m(N, K);
   return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 128 == 0 &&
          (long long)M * K < (1LL << 31) - 2048 && (long long)K * N < (1LL << 34);
 }

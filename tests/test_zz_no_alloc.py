@@ -36,7 +36,8 @@ def _mul(A, wt):
 
 
 # (M, K, N, group): mul_2_4 splits K on the first (decode, 64-column tiles in two
-# splits) and the third (large-M kernel, 16 tiles on 256 CUs); not on the second.
+# splits) and the third (large-M kernel, 32 tiles of 64 rows on 256 CUs, split three
+# ways); not on the second.
 CASES = [(16, 4096, 22016, 128), (4, 4096, 4096, 128), (256, 4096, 4096, -1), (1, 1024, 512, 128)]
 
 
