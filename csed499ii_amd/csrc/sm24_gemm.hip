@@ -595,11 +595,13 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 // MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
 struct DecodeShape {
   int tc, nw, splits;
+  int mb = 0;         // padded batch of the kernel (0: decode_batch(M))
   bool deep;          // register ring: deep (more stages in flight) or 16 VGPRs
   int tail_from = 0;  // > 0: only the tiles from this one are split (tail split)
   int cus = 0;        // compute units the grid runs on (LDS budget of resident rows)
 };
 bool decode_deep(int K, int splits);
+int decode_batch(int M);
 DecodeShape decode_shape(int M, int N, int K, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
@@ -608,7 +610,28 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   const bool wide32 = N / 32 >= 2 * cus;
   const bool narrow = 2 * (N / 64) < cus;
   const bool longk = K >= 8192;
-  if (narrow) {
+  // 5-8 rows: the 8-row batch (activations through LDS, as for 2-4 rows) where it
+  // measured faster than the 16-row one (M = 5 / 8, weights cold in HBM, one box:
+  // 7B o 4096x4096 5.22 / 5.23 -> 4.94 / 5.09 us with 16-column tiles of 8 waves;
+  // 7B gate_up 4096x22016 at M = 5 12.32 -> 11.45, but at M = 8 12.38 against 13.01,
+  // so up to 6 rows; 70B gate_up 8192x57344 38.1 / 39.6 -> 36.1 / 37.6; 70B qkv
+  // 8192x10240 11.7 / 12.3 -> 10.8 / 11.8).  The 16-row batch keeps 7B down and the
+  // 70B o and down shapes, and takes 64-column tiles of 8 waves for 7B qkv
+  // 4096x12288 (M = 5: 9.74 -> 7.56 us).
+  const bool mid = M >= 5 && M <= 8 && decode_batch(8) == 8;
+  if (mid && narrow && !longk && N / 16 >= cus) {
+    d = {16, 8, 1};
+    d.mb = 8;
+  } else if (mid && wide32 && (longk || M <= 6)) {
+    d = {longk ? 64 : 32, 4, 1};
+    d.mb = 8;
+  } else if (mid && longk && !wide32 && K < 16384 && N / 16 > 2 * cus) {
+    d = {32, 8, 1};
+    d.mb = 8;
+  } else if (mid && !longk && !narrow && !wide32) {
+    d = {64, 8, 1};
+    d.mb = 16;
+  } else if (narrow) {
     if (M > 16) d = {64, 4, 4};
     else if (longk && M > 4) d = {64, 8, 4};
     else d = {16, M <= 4 ? 8 : 4, 1};
@@ -638,6 +661,7 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   } else {
     d = {16, 4, 1};
   }
+  if (mid && d.mb == 0) d.mb = 16;  // the rest keep the 16-row batch
   if (forced_tc) d.tc = forced_tc;
   if (forced_nw) d.nw = forced_nw;
   if (forced_splits) d.splits = forced_splits;
@@ -703,9 +727,14 @@ void decode_unsplit(DecodeShape& d, int K) {
   d.deep = decode_deep(K, 1);
 }
 
-// Padded batch of the decode kernel: 1, 4 (activations staged through LDS), 16 or 32
-// (loaded straight into the MFMA operands: one or two 16-row blocks).
-int decode_batch(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
+// Padded batch of the decode kernel: 1, 4, 8 (activations staged through LDS), 16 or
+// 32 (loaded straight into the MFMA operands: one or two 16-row blocks).  The tile
+// table may raise 8 to 16 per shape.  MARLIN_HIP_DECODE_MB8=0 turns the 8-row batch
+// off (read once).
+int decode_batch(int M) {
+  static const int mb8 = env_choice("MARLIN_HIP_DECODE_MB8", {0, 1}, 1);
+  return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 && mb8 ? 8 : (M <= 16 ? 16 : 32)));
+}
 
 // Static LDS bytes of a kernel (cached per instantiation by the caller).
 size_t static_lds(const void* fn) {
@@ -766,18 +795,19 @@ void launch_decode_mb(const GemmArgs& a, bool deep, int vf, int mf, int cus, hip
 }
 
 template <int TC, int NW, bool GROUPED>
-void launch_decode_nw(const GemmArgs& a, bool deep, int vf, int mf, int cus, hipStream_t stream) {
-  const int mb = decode_batch(a.M);
+void launch_decode_nw(const GemmArgs& a, int mb, bool deep, int vf, int mf, int cus, hipStream_t stream) {
   if (mb == 1) launch_decode_mb<TC, NW, 1, GROUPED>(a, deep, vf, mf, cus, stream);
   else if (mb == 4) launch_decode_mb<TC, NW, 4, GROUPED>(a, deep, vf, mf, cus, stream);
+  else if (mb == 8) launch_decode_mb<TC, NW, 8, GROUPED>(a, deep, vf, mf, cus, stream);
   else if (mb == 16) launch_decode_mb<TC, NW, 16, GROUPED>(a, deep, vf, mf, cus, stream);
   else launch_decode_mb<TC, NW, 32, GROUPED>(a, deep, vf, mf, cus, stream);
 }
 
 template <int TC, bool GROUPED>
 hipError_t launch_decode_t(const GemmArgs& a, const DecodeShape& d, int vf, int mf, hipStream_t stream) {
-  if (d.nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, d.deep, vf, mf, d.cus, stream);
-  else launch_decode_nw<TC, 8, GROUPED>(a, d.deep, vf, mf, d.cus, stream);
+  const int mb = d.mb >= decode_batch(a.M) ? d.mb : decode_batch(a.M);
+  if (d.nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, mb, d.deep, vf, mf, d.cus, stream);
+  else launch_decode_nw<TC, 8, GROUPED>(a, mb, d.deep, vf, mf, d.cus, stream);
   return hipGetLastError();
 }
 
