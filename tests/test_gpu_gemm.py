@@ -287,6 +287,38 @@ def test_graph_replay_matches_eager(M, K, N):
         assert torch.equal(C, C_eager)
 
 
+@pytest.mark.parametrize("M,K,N,splits", [(256, 4096, 4096, 3), (200, 4096, 8192, 2)])
+def test_prefill_graph_replay_split_k(M, K, N, splits):
+    """Large-M calls on 64-row tiles split along K (the planner's choice for these
+    few-tile shapes; M = 200 leaves a ragged last tile), captured three times in one
+    graph on a warmed stream: four replays, each after eager work and a
+    synchronisation, equal the eager result bit for bit and the oracle."""
+    p = marlin.plan_2_4(M, K, N)
+    assert p["kernel"] == "large_m"
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert p["splits"] == splits and p["workgroups"] == splits * (N // 512) * -(-M // 64)
+    wt, A = _problem(M, N, K, 128, 77 + M)
+    ws = torch.zeros(N // 128 * 16, dtype=torch.int32, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        C_eager = torch.empty(M, N, dtype=torch.half, device=DEV)
+        marlin.mul_2_4(A, wt["B"], wt["meta"], C_eager, wt["s"], ws)
+    torch.cuda.synchronize()
+    _check(wt, A, C_eager, f"prefill split-K eager M={M} K={K} N={N}")
+    C = torch.zeros(M, N, dtype=torch.half, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(3):
+            marlin.mul_2_4(A, wt["B"], wt["meta"], C, wt["s"], ws)
+    for _ in range(4):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, C_eager)
+
+
 def test_layer_forward():
     K, N = 1024, 512
     gen = torch.Generator().manual_seed(3)
