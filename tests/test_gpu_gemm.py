@@ -203,6 +203,25 @@ def test_prefill_shape_slices(M):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"prefill M={M} slice {c0}")
 
 
+@pytest.mark.parametrize("M,K,N", [(33, 4096, 22016), (33, 8192, 10240), (65, 4096, 4096)])
+def test_prefill_from_few_rows(M, K, N):
+    """The large-M kernel at the smallest batches routed to it (from 33 rows for the
+    widest N and for long K at N >= 10240, from 65 at N >= 4096): one ragged 64-row
+    tile per 512 columns; first, middle and last column slices against the oracle,
+    and a repeated call is bit-identical."""
+    assert marlin.plan_2_4(M, K, N)["kernel"] == "large_m"
+    assert marlin.plan_2_4(M - 1, K, N)["kernel"] == "decode"
+    wt, A = _problem(M, N, K, 128, 4100 + M)
+    C = _run(wt, A)
+    assert torch.isfinite(C).all()
+    assert torch.equal(_run(wt, A), C), "repeated calls differ"
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2 - 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"prefill M={M} {K}x{N} slice {c0}")
+
+
 def test_deterministic_repeats():
     """Split-K reductions run in a fixed order: repeated calls are bit-identical
     (the reference's variant smoke test demands identical repeats)."""
