@@ -331,11 +331,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // st: the wave's stage buffer; dact: direct activation operands; aoff: byte offset
   // of the stage in the resident rows
   auto compute = [&](const uint8_t* st, const half8_t* dact, uint32_t aoff) {
-    // 4-bit path: every LDS operand of the stage is read before the first is used
-    // (the larger batches run one or two waves per SIMD, where a read per use
-    // exposes its whole latency)
-    constexpr bool HOIST = VF == VAL4 && MF == META4;
+    // 4-bit metadata (4- or 3-bit values): every LDS operand of the stage is read
+    // before the first is used (the larger batches run one or two waves per SIMD,
+    // where a read per use exposes its whole latency)
+    constexpr bool HOIST = MF == META4;
     uint32_t xr[KP][NCB][2];
+    uint32_t x3[KP][NCB][4];  // 3-bit values: the two word pairs of the lane's fields
     u32x2 mr[KP][NCB];
     _Float16 sr[NCB];
     if constexpr (HOIST) {
@@ -358,9 +359,20 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       for (int q2 = 0; q2 < KP; q2++)
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
-          const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
-          xr[q2][cb][0] = *reinterpret_cast<const uint32_t*>(vp);
-          xr[q2][cb][1] = *reinterpret_cast<const uint32_t*>(vp + 16);
+          if constexpr (VF == VAL4) {
+            const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
+            xr[q2][cb][0] = *reinterpret_cast<const uint32_t*>(vp);
+            xr[q2][cb][1] = *reinterpret_cast<const uint32_t*>(vp + 16);
+          } else {
+            const uint8_t* rowp = st + o_val + 2 * q2 * (BPK * 16);
+            const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
+            const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
+            const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
+            x3[q2][cb][0] = p0[0];
+            x3[q2][cb][1] = p0[1];
+            x3[q2][cb][2] = p1[0];
+            x3[q2][cb][3] = p1[1];
+          }
           mr[q2][cb] = *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
         }
       if constexpr (GROUPED) {
@@ -419,8 +431,10 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
           const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
           const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
-          const uint32_t y0 = __builtin_amdgcn_alignbit(p0[1], p0[0], 8 * (b0 & 3) + 6 * blk);
-          const uint32_t y1 = __builtin_amdgcn_alignbit(p1[1], p1[0], 8 * (b1 & 3) + 6 * blk);
+          const uint32_t y0 = __builtin_amdgcn_alignbit(HOIST ? x3[q2][cb][1] : p0[1], HOIST ? x3[q2][cb][0] : p0[0],
+                                                        8 * (b0 & 3) + 6 * blk);
+          const uint32_t y1 = __builtin_amdgcn_alignbit(HOIST ? x3[q2][cb][3] : p1[1], HOIST ? x3[q2][cb][2] : p1[0],
+                                                        8 * (b1 & 3) + 6 * blk);
           // One shift and one bit-field insert move the codes at bits 12 and 15 up to
           // 16 and 19, so that each half pair's codes sit 16 bits apart: masked and
           // or-ed with the magic exponent they are the halves 1024 + c (bits 0 / 16)
