@@ -331,12 +331,35 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // st: the wave's stage buffer; dact: direct activation operands; aoff: byte offset
   // of the stage in the resident rows
   auto compute = [&](const uint8_t* st, const half8_t* dact, uint32_t aoff) {
-    // 4-bit metadata (4- or 3-bit values): every LDS operand of the stage is read
-    // before the first is used (the larger batches run one or two waves per SIMD,
-    // where a read per use exposes its whole latency)
-    constexpr bool HOIST = MF == META4;
+    // Every LDS operand of the stage is read before the first is used (the larger
+    // batches run one or two waves per SIMD, where a read per use exposes its whole
+    // latency)
+    constexpr bool HOIST = true;
     uint32_t xr[KP][NCB][2];
     uint32_t x3[KP][NCB][4];  // 3-bit values: the two word pairs of the lane's fields
+    // 3-bit metadata: the code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf
+    // is the low (jb = 0) or high 24 bits of field "first" (g < 4) or "second"
+    // (g >= 4) at position P = u mod 16, in words (which, which+1); its two codes at
+    // pos and pos + 3 are Y:X shifted by the sum S (m3_shift), as one alignbit of Y:X
+    // (S < 32) or of Y:Y by S - 32 (only the low 6 bits are used).  m3_read returns
+    // Y and the low word L of that alignbit.
+    auto m3_which = [&](int cb) -> int { return TC == 64 ? (2 * cb + gl) >> 2 : g0 >> 2; };
+    auto m3_shift = [&](int cb) -> uint32_t { return m3_which(cb) == 0 ? m3s0 : m3s1; };
+    auto m3_read = [&](const uint8_t* stp, int q2, int cb, int ehalf, uint32_t& Y, uint32_t& L) {
+      const uint32_t* mrow = reinterpret_cast<const uint32_t*>(stp + o_mrow + 2 * q2 * (MPK * 16));
+      const int gt = 2 * cb + gl;
+      int ix, iy;  // words X = mrow[ix], Y = mrow[iy]
+      if constexpr (TC == 64) {
+        ix = 16 * m3_which(cb) + ((4 * gt + 2 * jj + ehalf) & 15);
+        iy = ix + 16;
+      } else {
+        ix = 4 * gt + 2 * jj + ehalf;
+        iy = ix + TC / 2;
+      }
+      Y = mrow[iy];
+      L = mrow[m3_shift(cb) >= 32u ? iy : ix];
+    };
+    uint32_t m3y[KP][NCB][2], m3l[KP][NCB][2];
     u32x2 mr[KP][NCB];
     _Float16 sr[NCB];
     if constexpr (HOIST) {
@@ -373,7 +396,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
             x3[q2][cb][2] = p1[0];
             x3[q2][cb][3] = p1[1];
           }
-          mr[q2][cb] = *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
+          if constexpr (MF == META4) {
+            mr[q2][cb] = *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
+          } else {
+#pragma unroll
+            for (int ehalf = 0; ehalf < 2; ehalf++) m3_read(st, q2, cb, ehalf, m3y[q2][cb][ehalf], m3l[q2][cb][ehalf]);
+          }
         }
       if constexpr (GROUPED) {
 #pragma unroll
@@ -473,28 +501,17 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           // of each ehalf go to selector bytes of one v_perm over the 8-byte nibble
           // table of its half (jb), which returns the four index nibbles as bytes,
           // then folded into the index halfword.
-          const uint32_t* mrow = reinterpret_cast<const uint32_t*>(st + o_mrow + 2 * q2 * (MPK * 16));
           uint32_t v[2];
 #pragma unroll
           for (int ehalf = 0; ehalf < 2; ehalf++) {
-            int which, ix, iy;  // words X = mrow[ix], Y = mrow[iy]
-            if constexpr (TC == 64) {
-              which = gt >> 2;
-              const int Pw = (4 * gt + 2 * jj + ehalf) & 15;
-              ix = 16 * which + Pw;
-              iy = ix + 16;
+            uint32_t Y, L;
+            if constexpr (HOIST) {
+              Y = m3y[q2][cb][ehalf];
+              L = m3l[q2][cb][ehalf];
             } else {
-              which = g0 >> 2;
-              ix = 4 * gt + 2 * jj + ehalf;
-              iy = ix + TC / 2;
+              m3_read(st, q2, cb, ehalf, Y, L);
             }
-            // the code word is Y:X >> {0, 24} (which 0, jb 0 / 1) or {16, 40} (which
-            // 1), its two codes at pos and pos + 3: Y:X shifted by the sum S, as one
-            // alignbit of Y:X (S < 32) or of Y:Y by S - 32 (only the low 6 bits are
-            // used)
-            const uint32_t S = which == 0 ? m3s0 : m3s1;
-            const uint32_t Y = mrow[iy], L = mrow[S >= 32u ? iy : ix];
-            v[ehalf] = __builtin_amdgcn_alignbit(Y, L, S & 31u);
+            v[ehalf] = __builtin_amdgcn_alignbit(Y, L, m3_shift(cb) & 31u);
           }
           // selector bytes {ca0, ca1, cb0, cb1} (code a / b of ehalf 0 / 1): the low
           // bytes of v[0], v[1] side by side, their b codes moved up by 13 bits
