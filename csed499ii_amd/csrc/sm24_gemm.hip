@@ -831,9 +831,12 @@ hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool 
 // M = 65 for N >= 4096 (M = 80 / 96: 7B qkv 23.0 / 22.8 against 28.4 / 31.7 us, 7B down
 // 28.2 / 28.5 against 30.3 / 32.8, 70B o 27.9 / 27.5 against 36.1 / 39.7; at M = 48 /
 // 64 the decode launches win for 7B o, down and qkv: 7B o 13.6 / 15.0 against 19.6 /
-// 20.0 us); M >= 160 for narrower N.  MARLIN_HIP_PREFILL_MIN_M (> 32) replaces the
+// 20.0 us); M >= 160 for narrower N.  MARLIN_HIP_PREFILL_MIN_M (>= 1) replaces the
 // threshold.
 int prefill_min_m(int N, int K) {
+  // the widest N at long K already from 17 rows (70B gate_up 8192x57344 at M = 24 /
+  // 32: 49.5 / 50.3 against 58.8 / 67.3 us; at M = 16 49.5 against 49.0)
+  if (N >= 16384 && K >= 8192) return 17;
   if (N >= 16384 || (N >= 10240 && K >= 8192)) return kDecodeMaxM + 1;
   return N >= 4096 ? 65 : 160;
 }
@@ -841,7 +844,7 @@ bool prefill_fits(int M, int N, int K, int vf, int mf) {
   static const int forced_min_m = [] {
     const char* e = getenv("MARLIN_HIP_PREFILL_MIN_M");
     const int x = e ? atoi(e) : 0;
-    return x > kDecodeMaxM ? x : 0;
+    return x >= 1 ? x : 0;
   }();
   const int min_m = forced_min_m ? forced_min_m : prefill_min_m(N, K);
   return vf == VAL4 && mf == META4 && M >= min_m && N % kPreTileCols == 0 && K % 128 == 0 &&
@@ -884,9 +887,8 @@ enum : int { KERNEL_DECODE = 0, KERNEL_PREFILL = 1, KERNEL_GENERAL = 2 };
 // against 49.7 us for the general kernel); the large-M kernel where it fits; the
 // general kernel otherwise.
 int kernel_for(int M, int N, int K) {
-  const bool chunked = M > kDecodeMaxM && M <= kDecodeChunkMaxM && !prefill_fits(M, N, K, VAL4, META4);
-  if (M <= kDecodeMaxM || chunked) return KERNEL_DECODE;
-  return prefill_fits(M, N, K, VAL4, META4) ? KERNEL_PREFILL : KERNEL_GENERAL;
+  if (prefill_fits(M, N, K, VAL4, META4)) return KERNEL_PREFILL;
+  return M <= kDecodeChunkMaxM ? KERNEL_DECODE : KERNEL_GENERAL;
 }
 
 // What run() launches for a 4-bit call when nothing limits its scratch:

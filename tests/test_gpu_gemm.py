@@ -150,8 +150,8 @@ def _weight70(K, N):
 @pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (28672, 8192), (8192, 57344)])
 def test_decode_llama70b_full_size_slices(K, N, M):
     """The Llama-2-70B decode shapes (long K: 32- and 64-column tiles, K unsplit or
-    split two or four ways), checked on column slices; repeated calls must be
-    bit-identical."""
+    split two or four ways; at M = 32 the widest shape, 8192x57344, runs the large-M
+    kernel), checked on column slices; repeated calls must be bit-identical."""
     wt, t = _weight70(K, N)
     A = synth.make_activation(M, K, 70 + M, device=DEV)
     C = _run(wt, A)
@@ -203,10 +203,11 @@ def test_prefill_shape_slices(M):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"prefill M={M} slice {c0}")
 
 
-@pytest.mark.parametrize("M,K,N", [(33, 4096, 22016), (33, 8192, 10240), (65, 4096, 4096)])
+@pytest.mark.parametrize("M,K,N", [(17, 8192, 57344), (33, 4096, 22016), (33, 8192, 10240), (65, 4096, 4096)])
 def test_prefill_from_few_rows(M, K, N):
-    """The large-M kernel at the smallest batches routed to it (from 33 rows for the
-    widest N and for long K at N >= 10240, from 65 at N >= 4096): one ragged 64-row
+    """The large-M kernel at the smallest batches routed to it (from 17 rows for the
+    widest N at long K, from 33 for the widest N and for long K at N >= 10240, from 65
+    at N >= 4096): one ragged 64-row
     tile per 512 columns; first, middle and last column slices against the oracle,
     and a repeated call is bit-identical."""
     assert marlin.plan_2_4(M, K, N)["kernel"] == "large_m"
