@@ -109,9 +109,10 @@ def test_ragged_batches(M):
     _check(wt, A, _run(wt, A), f"M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 6, 7, 8, 16])
 def test_config1_and_decode_o_proj(M):
-    """Benchmark config 1 (M=16) and the decode sweep at the O-projection shape."""
+    """Benchmark config 1 (M=16) and the decode sweep at the O-projection shape (5-8
+    rows: the 8-row batch, activation rows staged through LDS)."""
     wt, A = _problem(M, 4096, 4096, 128, 20261019 + M)
     _check(wt, A, _run(wt, A), f"4096^2 M={M}")
 
@@ -146,7 +147,7 @@ def _weight70(K, N):
     return _W70[(K, N)]
 
 
-@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 7, 8, 16, 32])
 @pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (28672, 8192), (8192, 57344)])
 def test_decode_llama70b_full_size_slices(K, N, M):
     """The Llama-2-70B decode shapes (long K: 32- and 64-column tiles, K unsplit or
