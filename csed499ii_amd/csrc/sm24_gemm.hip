@@ -460,7 +460,6 @@ __global__ __launch_bounds__(256) void w3_to_w4_kernel(const uint32_t* __restric
 // plus the exchange; it reproduces the measured times of every prefill-sweep call to
 // within ~5 % for both heights and 1-2 splits (forced by MARLIN_HIP_PREFILL_ROWS and
 // MARLIN_HIP_PREFILL_SPLITS, read once).  `nosplit`: one split only.
-int env_choice(const char* name, std::initializer_list<int> allowed, int fallback);
 struct PrefillPlan {
   int rows;    // batch rows per tile: 128 or 64
   int splits;  // K splits
@@ -593,15 +592,8 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 // CU) keeps 32-column tiles unsplit up to M = 8 (8.55 -> 7.47 us at M = 1).  The 7B
 // sweep (M in {1, 2, 4, 8, 16}) is within noise of the best forced choice per call.
 // MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
-struct DecodeShape {
-  int tc, nw, splits;
-  int mb = 0;         // padded batch of the kernel (0: decode_batch(M))
-  bool deep;          // register ring: deep (more stages in flight) or 16 VGPRs
-  int tail_from = 0;  // > 0: only the tiles from this one are split (tail split)
-  int cus = 0;        // compute units the grid runs on (LDS budget of resident rows)
-};
+
 bool decode_deep(int K, int splits);
-int decode_batch(int M);
 DecodeShape decode_shape(int M, int N, int K, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
@@ -734,81 +726,6 @@ void decode_unsplit(DecodeShape& d, int K) {
 int decode_batch(int M) {
   static const int mb8 = env_choice("MARLIN_HIP_DECODE_MB8", {0, 1}, 1);
   return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 && mb8 ? 8 : (M <= 16 ? 16 : 32)));
-}
-
-// Static LDS bytes of a kernel (cached per instantiation by the caller).
-size_t static_lds(const void* fn) {
-  hipFuncAttributes attr{};
-  return hipFuncGetAttributes(&attr, fn) == hipSuccess ? attr.sharedSizeBytes : SIZE_MAX;
-}
-
-// Batches of up to 4 rows keep their activation rows resident in LDS (one copy per
-// workgroup, loaded once: every stage's loads are weight pieces only) when a
-// workgroup runs at least 8 stages and the rows of its k range fit beside the
-// kernel's static LDS in 64 KiB, or in the CU's whole 160 KiB where the grid has at
-// most one workgroup per CU; otherwise each stage carries its activation pieces.
-// Measured on the Llama-2-7B shapes at M in {1, 2, 4}: 0.03-0.47 us faster per call
-// from 8 stages up (gate_up at M = 2: 10.09 -> 9.62 us), 0.07-0.23 us slower for o
-// 4096x4096 (4 stages of 32 k-blocks: the copy and its barrier are not amortised).
-// Beyond 64 KiB at one workgroup per CU: 7B down 11008x4096 at M = 2 / 4 (90 KiB of
-// rows) 7.01 -> 6.72 / 7.55 -> 7.18 us, Llama-2-70B o 8192x8192 (66 KiB) 8.63 ->
-// 7.47 / 8.64 -> 7.75 us; at two per CU (70B down, 57 KiB of rows each) it was
-// slower (20.05 -> 20.60 us at M = 4), so that case keeps the rows per stage.
-// MARLIN_HIP_DECODE_RES=0 turns it off.
-constexpr size_t kDecodeLdsMax = 64 * 1024;
-constexpr size_t kCuLds = 160 * 1024;  // LDS of one gfx950 compute unit
-template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
-void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
-  static const int forced_res = env_choice("MARLIN_HIP_DECODE_RES", {0, 1}, 1);
-  const int ntiles = a.N / TC;
-  const dim3 grid(a.tail_from > 0 ? a.tail_from + (ntiles - a.tail_from) * a.splits : ntiles * a.splits);
-  const dim3 block(64 * NW);
-  if constexpr (MB < 16) {
-    constexpr int ks = NW * (64 / TC > 2 ? 64 / TC : 2);
-    const int nst_all = (a.K / 32 + ks - 1) / ks;
-    const int nst_max = a.tail_from > 0 ? nst_all : (nst_all + a.splits - 1) / a.splits;
-    const size_t dyn = (size_t)MB * ((size_t)nst_max * ks * 64 + 16);
-    static const size_t stat =
-        static_lds(reinterpret_cast<const void*>(&sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>));
-    const bool fits = stat <= kCuLds && dyn <= kCuLds - stat &&
-                      (stat + dyn <= kDecodeLdsMax || (cus > 0 && grid.x <= (unsigned)cus));
-    if (forced_res == 1 && nst_max >= 8 && fits) {
-      hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>), grid, block, dyn, stream, a);
-      return;
-    }
-  }
-  hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream, a);
-}
-
-template <int TC, int NW, int MB, bool GROUPED>
-void launch_decode_mb(const GemmArgs& a, bool deep, int vf, int mf, int cus, hipStream_t stream) {
-  if (vf == VAL3) {
-    if (deep) launch_decode_v<TC, NW, MB, GROUPED, VAL3, META4, true>(a, cus, stream);
-    else launch_decode_v<TC, NW, MB, GROUPED, VAL3, META4, false>(a, cus, stream);
-  } else if (mf == META3) {
-    if (deep) launch_decode_v<TC, NW, MB, GROUPED, VAL4, META3, true>(a, cus, stream);
-    else launch_decode_v<TC, NW, MB, GROUPED, VAL4, META3, false>(a, cus, stream);
-  } else {
-    if (deep) launch_decode_v<TC, NW, MB, GROUPED, VAL4, META4, true>(a, cus, stream);
-    else launch_decode_v<TC, NW, MB, GROUPED, VAL4, META4, false>(a, cus, stream);
-  }
-}
-
-template <int TC, int NW, bool GROUPED>
-void launch_decode_nw(const GemmArgs& a, int mb, bool deep, int vf, int mf, int cus, hipStream_t stream) {
-  if (mb == 1) launch_decode_mb<TC, NW, 1, GROUPED>(a, deep, vf, mf, cus, stream);
-  else if (mb == 4) launch_decode_mb<TC, NW, 4, GROUPED>(a, deep, vf, mf, cus, stream);
-  else if (mb == 8) launch_decode_mb<TC, NW, 8, GROUPED>(a, deep, vf, mf, cus, stream);
-  else if (mb == 16) launch_decode_mb<TC, NW, 16, GROUPED>(a, deep, vf, mf, cus, stream);
-  else launch_decode_mb<TC, NW, 32, GROUPED>(a, deep, vf, mf, cus, stream);
-}
-
-template <int TC, bool GROUPED>
-hipError_t launch_decode_t(const GemmArgs& a, const DecodeShape& d, int vf, int mf, hipStream_t stream) {
-  const int mb = d.mb >= decode_batch(a.M) ? d.mb : decode_batch(a.M);
-  if (d.nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, mb, d.deep, vf, mf, d.cus, stream);
-  else launch_decode_nw<TC, 8, GROUPED>(a, mb, d.deep, vf, mf, d.cus, stream);
-  return hipGetLastError();
 }
 
 hipError_t launch_decode(const GemmArgs& a, DecodeShape d, int vf, int mf, bool grouped, hipStream_t stream) {

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
 #include <string>
 
 namespace sm24 {
@@ -40,5 +41,27 @@ struct DeviceScope {
     if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
   }
 };
+
+// Integer knob from the environment, read once per call site; `fallback` when unset
+// or not one of `allowed`.
+int env_choice(const char* name, std::initializer_list<int> allowed, int fallback);
+
+// Column-tile width, waves per workgroup and K splits of one decode launch (chosen by
+// decode_shape in sm24_gemm.hip).
+struct DecodeShape {
+  int tc, nw, splits;
+  int mb = 0;         // padded batch of the kernel (0: decode_batch(M))
+  bool deep;          // register ring: deep (more stages in flight) or 16 VGPRs
+  int tail_from = 0;  // > 0: only the tiles from this one are split (tail split)
+  int cus = 0;        // compute units the grid runs on (LDS budget of resident rows)
+};
+
+// Padded batch of the decode kernel for M rows: 1, 4, 8, 16 or 32.
+int decode_batch(int M);
+
+// Decode launch for one tile width and scale mode (sm24_decode_<TC>.hip).
+struct GemmArgs;
+template <int TC, bool GROUPED>
+hipError_t launch_decode_t(const GemmArgs& a, const DecodeShape& d, int vf, int mf, hipStream_t stream);
 
 }  // namespace sm24
