@@ -723,6 +723,81 @@ def floor_workload(args, device):
     return rows
 
 
+def spans_workload(args, device, shapes_70b=False):
+    """Per-wave phase timestamps of every decode-sweep call (the measurement build
+    ``libmarlin_hip_spans.so``, whose decode kernel records the 100 MHz real-time
+    counter at entry, once its first stages' loads are issued, after its last stage
+    and at exit).  Each call site is captured in a graph of 40 back-to-back calls
+    (weights rotating through their copies) whose last call carries the stamp buffer,
+    replayed 5 times; the last replay's stamps are summarised: span from the first
+    wave's entry to the last wave's exit, the spread of wave entries, and per wave the
+    median and maximum of the prologue (entry to first loads issued; its median
+    split into the wait for the kernel arguments, the load-address setup and the
+    issue of the first stages' loads), the main loop (to the last stage's MFMAs) and
+    the reduction and store (to exit)."""
+    from csed499ii_amd import build as _build
+
+    lib = _lib.load()
+    set_spans = lib.marlin_hip_set_spans
+    set_spans.restype = ctypes.c_int
+    set_spans.argtypes = [ctypes.c_void_p]
+    if set_spans(None) != 0:
+        raise SystemExit(f"{_lib.LIB_PATH.name} records no stamps: the spans workload needs {_build.SPANS_LIB.name}")
+    sub = argparse.Namespace(**vars(args))
+    sub.workload = "decode70b" if shapes_70b else "decode"
+    calls, _ = build_workload(sub, device)
+    rows = []
+    for c in calls:
+        plan = marlin.plan_2_4(c.M, c.K, c.N, 128)
+        waves = plan["threads"] // 64
+        nwaves = plan["workgroups"] * waves
+        buf = torch.zeros(nwaves * 12, dtype=torch.int64, device=device)
+        s = capture_stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            c()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(39):
+                c()
+            set_spans(ctypes.c_void_p(buf.data_ptr()))
+            try:
+                c()
+            finally:
+                set_spans(None)
+        for _ in range(5):
+            g.replay()
+        torch.cuda.synchronize()
+        t = buf.view(nwaves, 12).cpu().numpy().astype("int64")
+        del g
+        t0, targ, tset, t1, t2, t3, c0, c1 = (t[:, i] for i in range(8))
+        if (t0 == 0).any():
+            raise RuntimeError(f"spans: {c.name} M={c.M}: some waves recorded nothing")
+        import numpy as np
+
+        def med(x):
+            return round(float(np.median(x)) / 100.0, 3)  # 100 MHz ticks -> us
+
+        def mx(x):
+            return round(float(np.max(x)) / 100.0, 3)
+
+        clk = float(np.median((c1 - c0) / np.maximum(t3 - t0, 1))) * 100.0 / 1000.0  # GHz
+        row = {"name": c.name, "M": c.M, "K": c.K, "N": c.N, "workgroups": plan["workgroups"], "waves": waves,
+               "span_us": mx(t3 - t0.min()), "start_spread_us": mx(t0 - t0.min()),
+               "args_us": med(targ - t0), "setup_us": med(tset - targ), "issue_us": med(t1 - tset),
+               "prologue_us": med(t1 - t0), "prologue_max_us": mx(t1 - t0),
+               "loop_us": med(t2 - t1), "loop_max_us": mx(t2 - t1),
+               "tail_us": med(t3 - t2), "tail_max_us": mx(t3 - t2),
+               "wave_us": med(t3 - t0), "clock_GHz": round(clk, 2)}
+        rows.append(row)
+        log(f"bench: spans {c.name} M={c.M}: span {row['span_us']} us, start spread {row['start_spread_us']}, "
+            f"prologue {row['prologue_us']} (args {row['args_us']}, setup {row['setup_us']}, issue {row['issue_us']}; "
+            f"max {row['prologue_max_us']}), loop {row['loop_us']} "
+            f"(max {row['loop_max_us']}), tail {row['tail_us']} (max {row['tail_max_us']}), {row['clock_GHz']} GHz")
+    return rows
+
+
 def measure(args, wl, device, steps, warmup):
     """Build workload ``wl``, capture one step in a graph (or replay eagerly), time
     ``steps`` steps after ``warmup`` between two synchronisations.  Returns the
@@ -805,7 +880,7 @@ def main():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
                    choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "dense", "stack",
-                            "stack_native", "copy", "compare", "floor"])
+                            "stack_native", "copy", "compare", "floor", "spans", "spans70b"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
     p.add_argument("--no-prefill", action="store_true",
@@ -819,6 +894,10 @@ def main():
                          "Run with --gpus 1.")
     if not torch.cuda.is_available():
         raise SystemExit("no GPU visible")
+    if args.workload.startswith("spans"):
+        from csed499ii_amd import build as _build
+
+        _lib.LIB_PATH = _build.SPANS_LIB  # the measurement build (per-wave stamps)
     _lib.load()
     device = "cuda:0"
     log(f"bench: workload={args.workload} steps={args.steps} warmup={args.warmup}")
@@ -848,6 +927,20 @@ def main():
                                              "grid, reference timing protocol; value = the sweep's weight bytes "
                                              "over the summed read times",
                                      "empty_us_sum": round(sum(r["empty_us"] for r in rows), 3)},
+                          "per_call": rows}), flush=True)
+        return
+    if args.workload.startswith("spans"):
+        rows = spans_workload(args, device, shapes_70b=args.workload == "spans70b")
+        span = sum(r["span_us"] for r in rows)
+        wb = sum(synth.weight_bytes(r["K"], r["N"], 4, 128) for r in rows)
+        print(json.dumps({**base, "value": round(wb / (span * 1e3), 2), "unit": "GB/s", "steps": 0, "warmup": 0,
+                          "ms_per_step": round(span / 1e3, 4),
+                          "config": {"workload": "decode_sweep_llama2_%s_spans" % ("70b" if "70" in args.workload
+                                                                                  else "7b"),
+                                     "library": _lib.LIB_PATH.name,
+                                     "note": "per decode-sweep call: per-wave phase stamps of the last call of a "
+                                             "graph of 40; value = weight bytes over the summed spans (first "
+                                             "wave entry to last wave exit)"},
                           "per_call": rows}), flush=True)
         return
     res, pass_calls, cfg = measure(args, args.workload, device, args.steps, args.warmup)

@@ -18,6 +18,9 @@ PKG = pathlib.Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libmarlin_hip.so"
 PROBE_LIB = PKG / "libmarlin_probe.so"
+#: The same library with the decode kernel's per-wave phase timestamps compiled in
+#: (SM24_SPANS=1): a measurement build for ``bench.py --workload spans`` only.
+SPANS_LIB = PKG / "libmarlin_hip_spans.so"
 ARCH = "gfx950"
 
 
@@ -68,24 +71,30 @@ def _finish(proc: subprocess.Popen, what: str, verbose: bool) -> None:
 
 def build(verbose: bool = False) -> pathlib.Path:
     """Compile every source to an object (in parallel), then link
-    ``csed499ii_amd/libmarlin_hip.so`` (the GEMM library, from ``csrc/*.hip``) and
+    ``csed499ii_amd/libmarlin_hip.so`` (the GEMM library, from ``csrc/*.hip``),
+    ``csed499ii_amd/libmarlin_hip_spans.so`` (the same sources with SM24_SPANS=1: the
+    measurement build whose decode kernel records per-wave phase timestamps) and
     ``csed499ii_amd/libmarlin_probe.so`` (bench.py's measurement aids, from
-    ``csrc/probe/*.hip``); always rebuilds both."""
+    ``csrc/probe/*.hip``); always rebuilds all three."""
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     probe_srcs = sorted((CSRC / "probe").glob("*.hip"))
-    obj_dir = PKG / "_build"
-    obj_dir.mkdir(exist_ok=True)
-    objs, probe_objs, procs = [], [], []
-    for src in srcs + probe_srcs:
-        obj = obj_dir / (src.stem + ".o")
-        (probe_objs if src in probe_srcs else objs).append(obj)
-        cmd = [hipcc(), *compile_flags(), *EXTRA_FLAGS.get(src.name, []), "-c", "-o", str(obj), str(src)]
-        procs.append((_run(cmd, verbose), src.name))
+    variants = [(LIB, srcs, PKG / "_build", []), (SPANS_LIB, srcs, PKG / "_build_spans", ["-DSM24_SPANS=1"]),
+                (PROBE_LIB, probe_srcs, PKG / "_build", [])]
+    links, procs = [], []
+    for lib, lib_srcs, obj_dir, defs in variants:
+        obj_dir.mkdir(exist_ok=True)
+        objs = []
+        for src in lib_srcs:
+            obj = obj_dir / (src.stem + ".o")
+            objs.append(obj)
+            cmd = [hipcc(), *compile_flags(), *defs, *EXTRA_FLAGS.get(src.name, []), "-c", "-o", str(obj), str(src)]
+            procs.append((_run(cmd, verbose), src.name))
+        links.append((lib, objs))
     for proc, name in procs:
         _finish(proc, name, verbose)
-    for lib, lib_objs in ((LIB, objs), (PROBE_LIB, probe_objs)):
+    for lib, lib_objs in links:
         if not lib_objs:
             continue
         tmp = lib.with_suffix(".so.tmp")

@@ -1,4 +1,5 @@
-// Decode-sized (M <= 32) 2:4 INT4 x FP16 GEMM for gfx950.
+// Decode-sized 2:4 INT4 x FP16 GEMM for gfx950 at 1, 4 and 8 padded batch rows (up to
+// 8 rows per launch; 9-32 rows run sm24_decode_dma.h).
 //
 // One workgroup owns a tile of TC output columns (TC = 16, 32 or 64) over the whole
 // K, or over one of a.splits contiguous ranges of its stages (split-K, of every tile
@@ -14,16 +15,14 @@
 //
 // A stage covers KS = NW * KPW k-blocks of the tile, KPW = max(2, 64 / TC) per wave.
 // Each wave streams its own KPW k-blocks: their pieces - packed values, metadata,
-// the scales of their one scale group and, for MB < 16, the activation rows - form a
+// the scales of their one scale group and, unless resident, the activation rows - form a
 // list of P 16-byte pieces; lane l loads pieces l, l + 64, ... (SL slots) of every
 // stage, rows clamped to the operand, into a register ring D stages deep.  When a
 // stage is due the wave writes its pieces to one of its two LDS buffers and reads its
 // MFMA operands back: a wave's LDS operations complete in order, so no workgroup
-// barrier runs between stages.  For MB = 16 (32: two 16-row blocks, each weight
-// fragment feeding two MFMAs) every lane of the activation operand is a real batch
-// row, so each wave loads its activations straight into the ring instead.  Batch rows
-// past M read row M-1 (their outputs are not stored); k-blocks past K read zero
-// activations, so the last stage needs no per-k-block branch.
+// barrier runs between stages.  Batch rows past M read row M-1 (their outputs are not
+// stored); k-blocks past K read zero activations, so the last stage needs no
+// per-k-block branch.
 //
 // MFMA (v_smfmac_f32_16x16x64_f16, two k-blocks per instruction) lane roles: lane
 // (rho, h) = (l % 16, l / 16) holds output column n = n0 + 16*cb + rho, i.e. word j =
@@ -57,12 +56,11 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // of the 3-bit code words (the whole 192-byte group when TC == 64).
   constexpr int MPK = (MF == META3 && TC == 64) ? 12 : TC / 4;
   constexpr int SPG = TC / 8;                           // 16-byte scale pieces per scale group
-  // MB < 16: activations through LDS, either resident (RES: the workgroup's rows over
-  // its whole k range, loaded once by LDS-DMA into the dynamic LDS) or with every
-  // stage's pieces.  MB >= 16: loaded by each wave straight into its MFMA operands.
-  static_assert(!RES || MB < 16, "resident activations are for MB < 16");
-  constexpr bool STAGED = MB < 16 && !RES;              // activations with the stage pieces
-  constexpr int RB = MB > 16 ? MB / 16 : 1;             // 16-row batch blocks (MFMA B operands)
+  // Activations through LDS, either resident (RES: the workgroup's rows over its whole
+  // k range, loaded once by LDS-DMA into the dynamic LDS) or with every stage's pieces.
+  static_assert(MB == 1 || MB == 4 || MB == 8, "1, 4 or 8 padded batch rows");
+  constexpr bool STAGED = !RES;                         // activations with the stage pieces
+  constexpr int RB = 1;                                 // one 16-column MFMA B operand
   // Pieces of one wave's stage, in its LDS region in this order.
   constexpr int NB = KPW * BPK;
   constexpr int NM = KPW * MPK;
@@ -70,7 +68,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int NPA = STAGED ? KPW * 4 * MB : 0;        // activation pieces (4 per row and k-block)
   constexpr int P1 = NB + NM, P2 = P1 + NSC, P = P2 + NPA;
   constexpr int SL = (P + 63) / 64;                     // load slots per lane and stage
-  constexpr int DA = MB >= 16 ? KPW * RB : 0;          // direct activation loads per stage
   constexpr int MOFF = NB * 16, SOFF = MOFF + NM * 16, AOFF = SOFF + NSC * 16;
   constexpr int STAGE = AOFF + NPA * 16;                // bytes of one wave's stage
   static_assert(KPW <= 4 && 4 % KPW == 0, "a wave's k-blocks lie in one scale group");
@@ -79,10 +76,10 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // 8-wave or four 4-wave workgroups per CU).  Even, so that ring slot i always
   // uses LDS buffer i & 1 (consecutive stages must alternate buffers, also across
   // the wrap from slot D-1 to slot 0).
-  constexpr int LPS = SL + DA;
+  constexpr int LPS = SL;
   // DEEP: a ring as deep as the budget allows (long K: more bytes in flight per
   // workgroup); otherwise 16 VGPRs, so that more workgroups are resident per CU.
-  constexpr int RING_VGPRS = !DEEP ? 16 : (MB < 16 ? 40 : (RB > 1 || TC == 64 ? 48 : 64));
+  constexpr int RING_VGPRS = !DEEP ? 16 : 40;
   constexpr int D = cmax(2, cmin(16, cmin(56 / LPS, RING_VGPRS / (4 * LPS)))) & ~1;
   static_assert(D >= 2 && D % 2 == 0, "even ring depth");
   static_assert(KS % 4 == 0, "scale groups of 4 k-blocks per stage");
@@ -95,10 +92,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   constexpr int LDSB = 2 * NW * STAGE > REDB ? 2 * NW * STAGE : REDB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDSB];
 
+  SpanStamps sp;  // phase timestamps (measurement build only)
+  sp.mark(0);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int N = a.N, K = a.K, M = a.M;
+  sp.mark_args(N);
   const int nkb = K >> 5;
   const int ngroups = (nkb + 3) >> 2;
   // Split-K: split z of a tile covers stages [st0, st0 + nst) (the host keeps splits
@@ -276,13 +276,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   const uint32_t m3s0 = (jb ? 24u : 0u) + m3pos, m3s1 = (jb ? 40u : 16u) + m3pos;
   const uint32_t m3tlo = jb ? kTabLowLo : kTabHighLo, m3thi = jb ? kTabLowHi : kTabHighHi;
   const int arow = rho & (MB - 1);                   // staged activation row (lanes rho < MB)
-  // direct activation operands: batch rows rho + 16 rb (rows past M repeat row M-1)
-  const _Float16* abase[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; rb++) {
-    const int row = rho + 16 * rb;
-    abase[rb] = a.A + (size_t)(row < M ? row : M - 1) * K + 8 * au;
-  }
 
   // Per-lane LDS byte offsets of this wave's first k-block and column block; the
   // k-block pair (q2), column block (cb) and buffer parts are immediates.
@@ -304,14 +297,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   }
   asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(kMagic));
 
-  // direct load q = rb * KPW + (k-block of the wave's share)
-  auto load_direct = [&](int s, int q) -> half8_t {
-    const int rb = q / KPW;
-    const int kb = (st0 + s) * KS + wave * KPW + q % KPW;  // uniform
-    const _Float16* p = kb < nkb ? abase[rb] + 32 * kb : a.zeros;
-    return *reinterpret_cast<const half8_t*>(p);
-  };
-
   // one accumulator per k-block pair of a wave's share (no MFMA dependency chains)
   constexpr int KP = KPW / 2;
   float4_t acc[KP][NCB][RB];
@@ -328,9 +313,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // resident row of the lane (rho < M), at the wave's first k-block of stage 0
   const uint32_t o_ract = (uint32_t)arow * RS + (uint32_t)kw * 64u + 16u * au;
 
-  // st: the wave's stage buffer; dact: direct activation operands; aoff: byte offset
-  // of the stage in the resident rows
-  auto compute = [&](const uint8_t* st, const half8_t* dact, uint32_t aoff) {
+  // st: the wave's stage buffer; aoff: byte offset of the stage in the resident rows
+  auto compute = [&](const uint8_t* st, uint32_t aoff) {
     // Every LDS operand of the stage is read before the first is used (the larger
     // batches run one or two waves per SIMD, where a read per use exposes its whole
     // latency)
@@ -363,19 +347,17 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     u32x2 mr[KP][NCB];
     _Float16 sr[NCB];
     if constexpr (HOIST) {
-      if constexpr (MB < 16) {
 #pragma unroll
-        for (int q2 = 0; q2 < KP; q2++) {
-          if constexpr (RES) {
-            if (rho < M) {
-              const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
-              sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
-              sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(ap + 64);
-            }
-          } else if (rho < MB) {
-            sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
-            sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
+      for (int q2 = 0; q2 < KP; q2++) {
+        if constexpr (RES) {
+          if (rho < M) {
+            const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
+            sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
+            sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(ap + 64);
           }
+        } else if (rho < MB) {
+          sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
+          sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
         }
       }
 #pragma unroll
@@ -411,13 +393,12 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     }
 #pragma unroll
     for (int q2 = 0; q2 < KP; q2++) {
+      // Only lanes of real batch rows read the staged row; the other lanes' MFMA
+      // columns are never stored, so their operand keeps whatever the register held
+      // (LDS reads are paid per active lane).
       half16_t act[RB];
-      if constexpr (MB < 16) {
-        // Only lanes of real batch rows read the staged row; the other lanes' MFMA
-        // columns are never stored, so their operand keeps whatever the register
-        // held (LDS reads are paid per active lane).
-        if constexpr (HOIST) {
-        } else if constexpr (RES) {
+      if constexpr (!HOIST) {
+        if constexpr (RES) {
           if (rho < M) {
             const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
             sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
@@ -427,14 +408,9 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
           sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
         }
-        act[0] = __builtin_shufflevector(sact[2 * q2], sact[2 * q2 + 1], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12,
-                                         13, 14, 15);
-      } else {
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++)
-          act[rb] = __builtin_shufflevector(dact[rb * KPW + 2 * q2], dact[rb * KPW + 2 * q2 + 1], 0, 1, 2, 3, 4, 5, 6,
-                                            7, 8, 9, 10, 11, 12, 13, 14, 15);
       }
+      act[0] = __builtin_shufflevector(sact[2 * q2], sact[2 * q2 + 1], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14,
+                                       15);
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
         const int gt = 2 * cb + gl;
@@ -541,15 +517,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // stages D later, all unconditionally (stages past the end re-read the last rows:
   // the waits stay exact, which a conditional load would spoil).  The final round
   // issues no loads.
+  sp.mark(2);
   u32x4 ring[D][SL];
-  half8_t dring[D][DA > 0 ? DA : 1];
 #pragma unroll
   for (int i = 0; i < D; i++) {
 #pragma unroll
     for (int q = 0; q < SL; q++)
       if (slot_live(q)) ring[i][q] = load_slot(q, i);
-#pragma unroll
-    for (int q = 0; q < DA; q++) dring[i][q] = load_direct(i, q);
     __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (RES) {
@@ -558,6 +532,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     wait_vm<D * LPS>();
     __syncthreads();
   }
+  sp.mark(3);
   uint8_t* const wlds = lds + wave * 2 * STAGE;  // this wave's two stage buffers
   auto stage = [&](int i, bool reload, int s) {
     uint8_t* st = wlds + (i & 1) * STAGE;
@@ -569,11 +544,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    compute(st, dring[i], (uint32_t)s * (KS * 64));
-    if (reload) {
-#pragma unroll
-      for (int q = 0; q < DA; q++) dring[i][q] = load_direct(s + D, q);
-    }
+    compute(st, (uint32_t)s * (KS * 64));
     __builtin_amdgcn_sched_barrier(0);
   };
   int base = 0;
@@ -584,6 +555,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
 #pragma unroll
   for (int i = 0; i < D; i++)
     if (base + i < nst) stage(i, false, base + i);  // uniform
+  sp.mark(4);
 
 #pragma unroll
   for (int q = 1; q < KP; q++)
@@ -645,7 +617,10 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     __shared__ uint32_t arrived;
     if (tid == 0) arrived = __hip_atomic_fetch_add(a.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     __syncthreads();
-    if (arrived != (uint32_t)S) return;
+    if (arrived != (uint32_t)S) {
+      sp.store(a.spans, NW, wave, lane);
+      return;
+    }
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < 4 * TC && r_out < M) {
       // up to four splits' partials per batch of loads (the uncached reads are
@@ -668,6 +643,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       for (int rb = 0; rb < RB; rb++) write_c(rb, v[rb]);
     }
   }
+  sp.store(a.spans, NW, wave, lane);
 }
 
 }  // namespace sm24

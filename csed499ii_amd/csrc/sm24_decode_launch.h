@@ -1,9 +1,10 @@
-// Launchers of the decode kernel (sm24_decode.h), instantiated per tile width in
-// sm24_decode_16.hip, sm24_decode_32.hip and sm24_decode_64.hip so that the library's
-// translation units compile in parallel; sm24_gemm.hip's launch_decode dispatches to
-// them.
+// Launchers of the decode kernels (sm24_decode.h for 1, 4 and 8 padded rows,
+// sm24_decode_dma.h for 16 and 32), instantiated per tile width in sm24_decode_16.hip,
+// sm24_decode_32.hip and sm24_decode_64.hip so that the library's translation units
+// compile in parallel; sm24_gemm.hip's launch_decode dispatches to them.
 #pragma once
 #include "sm24_decode.h"
+#include "sm24_decode_dma.h"
 #include "sm24_host.h"
 
 namespace sm24 {
@@ -31,11 +32,17 @@ constexpr size_t kDecodeLdsMax = 64 * 1024;
 constexpr size_t kCuLds = 160 * 1024;  // LDS of one gfx950 compute unit
 template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
 void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
-  static const int forced_res = env_choice("MARLIN_HIP_DECODE_RES", {0, 1}, 1);
   const int ntiles = a.N / TC;
   const dim3 grid(a.tail_from > 0 ? a.tail_from + (ntiles - a.tail_from) * a.splits : ntiles * a.splits);
   const dim3 block(64 * NW);
-  if constexpr (MB < 16) {
+  if constexpr (MB >= 16) {
+    // 16 and 32 padded rows: the LDS-DMA kernel (sm24_decode_dma.h).  Its activation
+    // pieces travel with each stage into LDS; against the register-ring kernel with
+    // direct activation operands (same tile table, same box): Llama-2-7B at M = 16 qkv
+    // 8.37 -> 7.71, o 6.54 -> 5.88, gate_up 12.21 -> 11.35, down 9.30 -> 8.71 us.
+    hipLaunchKernelGGL((sm24_decode_dma_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP>), grid, block, 0, stream, a);
+  } else {
+    static const int forced_res = env_choice("MARLIN_HIP_DECODE_RES", {0, 1}, 1);
     constexpr int ks = NW * (64 / TC > 2 ? 64 / TC : 2);
     const int nst_all = (a.K / 32 + ks - 1) / ks;
     const int nst_max = a.tail_from > 0 ? nst_all : (nst_all + a.splits - 1) / a.splits;
@@ -48,8 +55,8 @@ void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
       hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>), grid, block, dyn, stream, a);
       return;
     }
+    hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream, a);
   }
-  hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream, a);
 }
 
 template <int TC, int NW, int MB, bool GROUPED>

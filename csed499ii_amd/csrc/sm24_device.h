@@ -121,6 +121,66 @@ struct GemmArgs {
   int tail_from;   // decode: first split tile (0: every tile split when splits > 1)
   float* partial;  // [splits][M][N] when splits > 1
   uint32_t* counters;  // [gridDim.z][gridDim.x] arrival counters, zero between launches
+  uint64_t* spans;     // per-wave timestamps (only read by a build with SM24_SPANS=1)
+};
+
+// Per-wave phase timestamps of the decode kernel, compiled in only by the
+// measurement build (SM24_SPANS=1, libmarlin_hip_spans.so): wave w of workgroup b
+// writes kSpanWords 64-bit words at spans[(b * waves + w) * kSpanWords]: the 100 MHz
+// real-time counter at entry (stamp 0), once the kernel arguments have arrived (1),
+// once its load addresses are set up (2), once its first stages' loads are issued
+// (3), after its last stage's MFMAs (4) and at exit (5); the shader clock at entry
+// and exit; the hardware id of its compute unit; and the workgroup index.  Lane 0
+// stores them with vector stores.
+#ifndef SM24_SPANS
+#define SM24_SPANS 0
+#endif
+constexpr int kSpanStamps = 6;
+constexpr int kSpanWords = 12;
+struct SpanStamps {
+#if SM24_SPANS
+  uint64_t t[kSpanStamps] = {};
+  uint64_t c0 = 0;
+#endif
+  __device__ __forceinline__ void mark(int i) {
+#if SM24_SPANS
+    __builtin_amdgcn_sched_barrier(0);
+    t[i] = __builtin_amdgcn_s_memrealtime();
+    if (i == 0) c0 = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_sched_barrier(0);
+#else
+    (void)i;
+#endif
+  }
+  // stamp 1: waits for a kernel argument first
+  __device__ __forceinline__ void mark_args(int arg) {
+#if SM24_SPANS
+    asm volatile("" ::"s"(arg));
+    mark(1);
+#else
+    (void)arg;
+#endif
+  }
+  __device__ __forceinline__ void store(uint64_t* spans, int waves, int wave, int lane) {
+#if SM24_SPANS
+    mark(kSpanStamps - 1);
+    const uint64_t c1 = __builtin_amdgcn_s_memtime();
+    if (spans != nullptr && lane == 0) {
+      uint64_t* o = spans + ((size_t)blockIdx.x * waves + wave) * kSpanWords;
+      uint64_t v[kSpanWords] = {};
+#pragma unroll
+      for (int i = 0; i < kSpanStamps; i++) v[i] = t[i];
+      v[6] = c0;
+      v[7] = c1;
+      v[8] = (uint64_t)__smid();
+      v[9] = (uint64_t)blockIdx.x;
+#pragma unroll
+      for (int i = 0; i < kSpanWords; i++) __builtin_nontemporal_store(v[i], o + i);
+    }
+#else
+    (void)spans, (void)waves, (void)wave, (void)lane;
+#endif
+  }
 };
 
 // Large-M kernel (sm24_prefill.hip): output columns per workgroup tile (N must be a

@@ -35,6 +35,7 @@
 #include "sm24_host.h"
 #include "sm24_native.h"
 #include "../../include/marlin_hip.h"
+#include "../../include/marlin_spans.h"
 
 namespace sm24 {
 
@@ -296,6 +297,10 @@ __global__ __launch_bounds__(64 * NW) void sm24_gemm_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 
 thread_local std::string g_last_error;
+
+// Buffer for the decode kernel's per-wave phase timestamps (marlin_hip_set_spans;
+// recorded only by the measurement build).
+uint64_t* g_spans = nullptr;
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -884,6 +889,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       d.s = static_cast<const _Float16*>(s);
       d.C = static_cast<_Float16*>(C) + (size_t)r0 * N;
       d.zeros = zeros;
+      d.spans = g_spans;
       d.M = mc;
       d.N = N;
       d.K = K;
@@ -1242,5 +1248,10 @@ int marlin_hip_mul_2_4_w3(const void* A, const void* B3, const void* meta, void*
 }
 
 const char* marlin_hip_last_error(void) { return sm24::g_last_error.c_str(); }
+
+int marlin_hip_set_spans(void* buf) {
+  sm24::g_spans = static_cast<uint64_t*>(buf);
+  return SM24_SPANS ? MARLIN_HIP_OK : MARLIN_HIP_ERR_KERN_SHAPE;
+}
 
 }  // extern "C"

@@ -159,3 +159,23 @@ def test_dense_host_validation_codes(built_lib, args, expected):
     m, n, k, g, tk, tn = args
     null = ctypes.c_void_p(0)
     assert built_lib.marlin_hip_mul(null, null, null, null, m, n, k, null, g, 0, null, tk, tn, -1, 16) == expected
+
+
+def test_spans_hook(built_lib):
+    """The measurement hook of include/marlin_spans.h: exported by the product library
+    (which records no stamps: code 2) and by the measurement build (code 0); setting
+    it launches nothing, so this runs without a GPU."""
+    from csed499ii_amd import build
+
+    header = (HEADER.parent / "marlin_spans.h").read_text()
+    assert re.findall(r"^\s*int\s+(marlin_hip_\w+)\s*\(", header, re.M) == ["marlin_hip_set_spans"]
+    fn = built_lib.marlin_hip_set_spans
+    fn.restype, fn.argtypes = ctypes.c_int, [ctypes.c_void_p]
+    assert fn(None) == _lib.ERR_KERN_SHAPE
+    spans = ctypes.CDLL(str(build.SPANS_LIB))
+    spans.marlin_hip_set_spans.restype, spans.marlin_hip_set_spans.argtypes = ctypes.c_int, [ctypes.c_void_p]
+    assert spans.marlin_hip_set_spans(None) == _lib.OK
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.SPANS_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT\s+(marlin_hip_\w+)", out))
+    assert set(declared_symbols()) <= exported
