@@ -689,19 +689,82 @@ def load_probe():
         lib.marlin_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_void_p]
         lib.marlin_probe_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-        ProbeRead.lib = ProbeEmpty.lib = lib
+        lib.marlin_probe_smfmac_stream.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                                   ctypes.c_int, ctypes.c_void_p]
+        ProbeRead.lib = ProbeEmpty.lib = SmfmacStream.lib = lib
     return ProbeRead.lib
 
 
-def floor_workload(args, device):
-    """The per-call floor of the decode sweep: for every (shape, M) call, a streaming
-    read of exactly its weight bytes (best of several grid sizes) and an empty kernel
-    on its planned grid, each timed by the reference protocol.  The floor of a call
-    is the read (a kernel that moves those bytes cannot take less); the empty kernel
-    is its launch share."""
+class SmfmacStream:
+    """The mfma_floor workload's stand-in for one prefill call: the MFMA-only stream of
+    libmarlin_probe.so on the call's planned grid (workgroups of 8 waves, 128
+    accumulator AGPRs each), with as many v_smfmac_f32_32x32x32_f16 per SIMD as the
+    call issues (16 per wave and 64-deep k-step for 128-row tiles, 8 for 64-row)."""
+
+    lib = None
+
+    def __init__(self, c, device):
+        self.name, self.K, self.N, self.M = c.name, c.K, c.N, c.M
+        self.wbytes, self.kb_bytes, self.flops = 0, 0, c.flops
+        self.plan = marlin.plan_2_4(c.M, c.K, c.N, 128)
+        tiles = self.plan["workgroups"] // self.plan["splits"]
+        self.rows = 128 if tiles == (c.N // 512) * -(-c.M // 128) else 64
+        ksteps = -(-(c.K // 64) // self.plan["splits"])
+        self.iters = max(1, ksteps * self.rows // 128)
+        self.dev = torch.device(device).index or 0
+        self.out = torch.zeros(self.plan["workgroups"] * 8, dtype=torch.float32, device=device)
+        self.clock = torch.zeros(4, dtype=torch.int64, device=device)
+        self.wset = None
+
+    def __call__(self):
+        err = self.lib.marlin_probe_smfmac_stream(self.plan["workgroups"], self.iters,
+                                                  ctypes.c_void_p(self.out.data_ptr()),
+                                                  ctypes.c_void_p(self.clock.data_ptr()), self.dev,
+                                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if err:
+            raise RuntimeError(f"marlin_probe_smfmac_stream error {err}")
+
+
+def mfma_floor_workload(args, device, cus=256):
+    """The compute ceiling of the prefill sweep: per call, the MFMA-only smfmac stream
+    on the call's grid (SmfmacStream) beside the call itself, both by the reference
+    protocol.  The stream's clock is its wave 0's shader clock against the real-time
+    counter (one sample per call); cycles per smfmac = clock x time / (rounds of
+    workgroups over the CUs x smfmacs per SIMD: 2 waves x 16 per iteration)."""
     load_probe()
     sub = argparse.Namespace(**vars(args))
-    sub.workload = "decode"
+    sub.workload = "prefill"
+    calls, _ = build_workload(sub, device)
+    rows = []
+    for c in calls:
+        st = SmfmacStream(c, device)
+        su = per_call_stats([st], samples=5, replays=2, reps=4)[0]["us"]
+        cl = st.clock.cpu().tolist()
+        ghz = (cl[2] - cl[0]) / max(cl[3] - cl[1], 1) * 0.1  # 100 MHz real-time ticks
+        gu = per_call_stats([c], samples=5, replays=2, reps=4)[0]["us"]
+        rounds = -(-st.plan["workgroups"] // cus)
+        smf = rounds * st.iters * 32
+        rows.append({"name": c.name, "M": c.M, "K": c.K, "N": c.N, "tile_rows": st.rows,
+                     "splits": st.plan["splits"], "workgroups": st.plan["workgroups"],
+                     "stream_us": su, "stream_TFLOPs": round(c.flops / (su * 1e6), 1),
+                     "stream_clock_GHz": round(ghz, 2),
+                     "stream_cycles_per_smfmac": round(ghz * 1e3 * su / smf, 1),
+                     "gemm_us": gu, "gemm_TFLOPs": round(c.flops / (gu * 1e6), 1),
+                     "gemm_of_stream": round(su / gu, 3)})
+        log(f"bench: mfma floor {c.name} M={c.M}: stream {su:.1f} us ({rows[-1]['stream_TFLOPs']} TFLOP/s, "
+            f"{ghz:.2f} GHz, {rows[-1]['stream_cycles_per_smfmac']} cycles/smfmac), gemm {gu:.1f} us")
+    return rows
+
+
+def floor_workload(args, device, shapes_70b=False):
+    """The per-call floor of the decode sweep (Llama-2-7B shapes, or -70B with
+    ``shapes_70b``): for every (shape, M) call, a streaming read of exactly its weight
+    bytes (best of several grid sizes) and an empty kernel on its planned grid, each
+    timed by the reference protocol.  The floor of a call is the read (a kernel that
+    moves those bytes cannot take less); the empty kernel is its launch share."""
+    load_probe()
+    sub = argparse.Namespace(**vars(args))
+    sub.workload = "decode70b" if shapes_70b else "decode"
     calls, _ = build_workload(sub, device)
     pool = torch.empty(int(MALL_BYTES * 1.5) + (64 << 20), dtype=torch.uint8, device=device)
     pool.random_(0, 256)
@@ -709,7 +772,7 @@ def floor_workload(args, device):
     rows = []
     for c in calls:
         best = None
-        for blocks in (256, 512, 1024, 2048):
+        for blocks in (256, 512, 1024, 2048, -256, -512, -1024, -2048):  # < 0: a contiguous range per wave
             r = per_call_stats([ProbeRead(c, pool, sink, blocks)])[0]
             if best is None or r["us"] < best[0]:
                 best = (r["us"], blocks)
@@ -718,23 +781,94 @@ def floor_workload(args, device):
         rows.append({"name": c.name, "M": c.M, "K": c.K, "N": c.N, "read_us": best[0], "read_blocks": best[1],
                      "read_GBps": round(c.wbytes / (best[0] * 1e3), 1), "empty_us": eu,
                      "workgroups": e.plan["workgroups"], "threads": e.plan["threads"]})
-        log(f"bench: floor {c.name} M={c.M}: read {best[0]:.2f} us ({best[1]} blocks), empty {eu:.2f} us")
+        log(f"bench: floor {c.name} M={c.M}: read {best[0]:.2f} us ({abs(best[1])} blocks, "
+            f"{'per-wave ranges' if best[1] < 0 else 'grid stride'}), empty {eu:.2f} us")
     del pool
     return rows
 
 
-def spans_workload(args, device, shapes_70b=False):
+def span_row(c, plan, t):
+    """Summary of one launch's per-wave stamps ``t`` [waves, 12] (see spans_workload)."""
+    import numpy as np
+
+    t0, targ, tset, t1, t2, t3, c0, c1 = (t[:, i] for i in range(8))
+    if (t0 == 0).any():
+        raise RuntimeError(f"spans: {c.name} M={c.M}: some waves recorded nothing")
+
+    def med(x):
+        return round(float(np.median(x)) / 100.0, 3)  # 100 MHz ticks -> us
+
+    def mx(x):
+        return round(float(np.max(x)) / 100.0, 3)
+
+    clk = float(np.median((c1 - c0) / np.maximum(t3 - t0, 1))) * 100.0 / 1000.0  # GHz
+    return {"name": c.name, "M": c.M, "K": c.K, "N": c.N, "workgroups": plan["workgroups"],
+            "waves": plan["threads"] // 64,
+            "span_us": mx(t3 - t0.min()), "start_spread_us": mx(t0 - t0.min()),
+            "args_us": med(targ - t0), "setup_us": med(tset - targ), "issue_us": med(t1 - tset),
+            "prologue_us": med(t1 - t0), "prologue_max_us": mx(t1 - t0),
+            "loop_us": med(t2 - t1), "loop_max_us": mx(t2 - t1),
+            "tail_us": med(t3 - t2), "tail_max_us": mx(t3 - t2),
+            "wave_us": med(t3 - t0), "clock_GHz": round(clk, 2),
+            "first_start": int(t0.min()), "last_end": int(t3.max())}
+
+
+def spans_in_sweep(calls, set_spans, device):
+    """Stamps of every call of one pass of the bench's decode graph (the default
+    workload's step: the calls back to back, weights rotating), each call with its
+    own buffer; the last of 5 replays.  Adds the gap from the previous call's last
+    wave exit to this call's first wave entry."""
+    plans = [marlin.plan_2_4(c.M, c.K, c.N, 128) for c in calls]
+    bufs = [torch.zeros(p["workgroups"] * (p["threads"] // 64) * 12, dtype=torch.int64, device=device)
+            for p in plans]
+    s = capture_stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    for c in calls:
+        c.wset.reset()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        try:
+            for c, b in zip(calls, bufs):
+                set_spans(ctypes.c_void_p(b.data_ptr()))
+                c()
+        finally:
+            set_spans(None)
+    for _ in range(5):
+        g.replay()
+    torch.cuda.synchronize()
+    rows, prev_end = [], None
+    for c, p, b in zip(calls, plans, bufs):
+        r = span_row(c, p, b.view(-1, 12).cpu().numpy().astype("int64"))
+        r["gap_us"] = None if prev_end is None else round((r["first_start"] - prev_end) / 100.0, 3)
+        prev_end = r["last_end"]
+        rows.append(r)
+        log(f"bench: sweep spans {c.name} M={c.M}: gap {r['gap_us']} us, span {r['span_us']} us, "
+            f"start spread {r['start_spread_us']}, prologue {r['prologue_us']} (args {r['args_us']}, "
+            f"setup {r['setup_us']}, issue {r['issue_us']}), loop {r['loop_us']} (max {r['loop_max_us']}), "
+            f"tail {r['tail_us']} (max {r['tail_max_us']})")
+    del g
+    return rows
+
+
+def spans_workload(args, device, shapes_70b=False, in_sweep=False):
     """Per-wave phase timestamps of every decode-sweep call (the measurement build
     ``libmarlin_hip_spans.so``, whose decode kernel records the 100 MHz real-time
     counter at entry, once its first stages' loads are issued, after its last stage
     and at exit).  Each call site is captured in a graph of 40 back-to-back calls
-    (weights rotating through their copies) whose last call carries the stamp buffer,
-    replayed 5 times; the last replay's stamps are summarised: span from the first
-    wave's entry to the last wave's exit, the spread of wave entries, and per wave the
+    (weights rotating through their copies) whose last two calls carry stamp buffers,
+    replayed 5 times; the last replay's stamps are summarised: the gap from the
+    previous call's last wave exit to this call's first wave entry, the span from the
+    first wave's entry to the last wave's exit, the spread of wave entries, and per
+    wave the
     median and maximum of the prologue (entry to first loads issued; its median
     split into the wait for the kernel arguments, the load-address setup and the
     issue of the first stages' loads), the main loop (to the last stage's MFMAs) and
-    the reduction and store (to exit)."""
+    the reduction and store (to exit).  ``in_sweep``: the same for every call of one
+    pass of the default workload's graph (spans_in_sweep)."""
     from csed499ii_amd import build as _build
 
     lib = _lib.load()
@@ -746,11 +880,14 @@ def spans_workload(args, device, shapes_70b=False):
     sub = argparse.Namespace(**vars(args))
     sub.workload = "decode70b" if shapes_70b else "decode"
     calls, _ = build_workload(sub, device)
+    if in_sweep:
+        return spans_in_sweep(calls, set_spans, device)
     rows = []
     for c in calls:
         plan = marlin.plan_2_4(c.M, c.K, c.N, 128)
         waves = plan["threads"] // 64
         nwaves = plan["workgroups"] * waves
+        prev = torch.zeros(nwaves * 12, dtype=torch.int64, device=device)
         buf = torch.zeros(nwaves * 12, dtype=torch.int64, device=device)
         s = capture_stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -759,39 +896,24 @@ def spans_workload(args, device, shapes_70b=False):
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
-            for _ in range(39):
+            for _ in range(38):
                 c()
-            set_spans(ctypes.c_void_p(buf.data_ptr()))
             try:
-                c()
+                for b in (prev, buf):
+                    set_spans(ctypes.c_void_p(b.data_ptr()))
+                    c()
             finally:
                 set_spans(None)
         for _ in range(5):
             g.replay()
         torch.cuda.synchronize()
         t = buf.view(nwaves, 12).cpu().numpy().astype("int64")
+        prev_end = int(prev.view(nwaves, 12)[:, 5].max())
         del g
-        t0, targ, tset, t1, t2, t3, c0, c1 = (t[:, i] for i in range(8))
-        if (t0 == 0).any():
-            raise RuntimeError(f"spans: {c.name} M={c.M}: some waves recorded nothing")
-        import numpy as np
-
-        def med(x):
-            return round(float(np.median(x)) / 100.0, 3)  # 100 MHz ticks -> us
-
-        def mx(x):
-            return round(float(np.max(x)) / 100.0, 3)
-
-        clk = float(np.median((c1 - c0) / np.maximum(t3 - t0, 1))) * 100.0 / 1000.0  # GHz
-        row = {"name": c.name, "M": c.M, "K": c.K, "N": c.N, "workgroups": plan["workgroups"], "waves": waves,
-               "span_us": mx(t3 - t0.min()), "start_spread_us": mx(t0 - t0.min()),
-               "args_us": med(targ - t0), "setup_us": med(tset - targ), "issue_us": med(t1 - tset),
-               "prologue_us": med(t1 - t0), "prologue_max_us": mx(t1 - t0),
-               "loop_us": med(t2 - t1), "loop_max_us": mx(t2 - t1),
-               "tail_us": med(t3 - t2), "tail_max_us": mx(t3 - t2),
-               "wave_us": med(t3 - t0), "clock_GHz": round(clk, 2)}
+        row = span_row(c, plan, t)
+        row["gap_us"] = round((row["first_start"] - prev_end) / 100.0, 3)  # from the previous call's last exit
         rows.append(row)
-        log(f"bench: spans {c.name} M={c.M}: span {row['span_us']} us, start spread {row['start_spread_us']}, "
+        log(f"bench: spans {c.name} M={c.M}: gap {row['gap_us']} us, span {row['span_us']} us, start spread {row['start_spread_us']}, "
             f"prologue {row['prologue_us']} (args {row['args_us']}, setup {row['setup_us']}, issue {row['issue_us']}; "
             f"max {row['prologue_max_us']}), loop {row['loop_us']} "
             f"(max {row['loop_max_us']}), tail {row['tail_us']} (max {row['tail_max_us']}), {row['clock_GHz']} GHz")
@@ -880,7 +1002,8 @@ def main():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
                    choices=["decode", "decode70b", "native", "native70b", "prefill", "w3", "meta3", "dense", "stack",
-                            "stack_native", "copy", "compare", "floor", "spans", "spans70b"])
+                            "stack_native", "copy", "compare", "floor", "floor70b", "mfma_floor", "spans", "spans70b",
+                            "spans_sweep"])
     p.add_argument("--eager", action="store_true", help="replay the calls without a HIP graph")
     p.add_argument("--prefill-m", type=int, nargs="+", default=[512, 1024, 2048, 4096])
     p.add_argument("--no-prefill", action="store_true",
@@ -915,22 +1038,40 @@ def main():
                                              "library's decode call sites (M in {1, 16}) on weight bytes"},
                           "compare": rows}), flush=True)
         return
-    if args.workload == "floor":
-        rows = floor_workload(args, device)
+    if args.workload == "mfma_floor":
+        rows = mfma_floor_workload(args, device)
+        fl = sum(2 * r["M"] * r["K"] * r["N"] for r in rows)
+        su = sum(r["stream_us"] for r in rows)
+        gu = sum(r["gemm_us"] for r in rows)
+        print(json.dumps({**base, "value": round(fl / (su * 1e6), 1), "unit": "TFLOP/s", "steps": 0, "warmup": 0,
+                          "ms_per_step": round(su / 1e3, 4),
+                          "config": {"workload": "prefill_sweep_llama2_70b_mfma_floor",
+                                     "note": "per prefill-sweep call: the MFMA-only smfmac 32x32x32 stream on its "
+                                             "planned grid with the call's smfmac count, reference timing "
+                                             "protocol; value = the sweep's dense-equivalent FLOPs over the summed "
+                                             "stream times",
+                                     "gemm_TFLOPs": round(fl / (gu * 1e6), 1)},
+                          "per_call": rows}), flush=True)
+        return
+    if args.workload in ("floor", "floor70b"):
+        rows = floor_workload(args, device, shapes_70b=args.workload == "floor70b")
         wb = sum(synth.weight_bytes(r["K"], r["N"], 4, 128) for r in rows)
         read_us = sum(r["read_us"] for r in rows)
         print(json.dumps({**base, "value": round(wb / (read_us * 1e3), 2), "unit": "GB/s", "steps": 0,
                           "warmup": 0, "ms_per_step": round(read_us / 1e3, 4),
-                          "config": {"workload": "decode_sweep_llama2_7b_floor",
+                          "config": {"workload": "decode_sweep_llama2_%s_floor" % (
+                                         "70b" if args.workload == "floor70b" else "7b"),
                                      "note": "per decode-sweep call: a plain streaming read of its weight bytes "
-                                             "(best of 256-2048 workgroups) and an empty kernel on its planned "
+                                             "(best of 256-2048 workgroups, grid-stride order or a contiguous "
+                                             "range per wave: read_blocks < 0) and an empty kernel on its planned "
                                              "grid, reference timing protocol; value = the sweep's weight bytes "
                                              "over the summed read times",
                                      "empty_us_sum": round(sum(r["empty_us"] for r in rows), 3)},
                           "per_call": rows}), flush=True)
         return
     if args.workload.startswith("spans"):
-        rows = spans_workload(args, device, shapes_70b=args.workload == "spans70b")
+        rows = spans_workload(args, device, shapes_70b=args.workload == "spans70b",
+                              in_sweep=args.workload == "spans_sweep")
         span = sum(r["span_us"] for r in rows)
         wb = sum(synth.weight_bytes(r["K"], r["N"], 4, 128) for r in rows)
         print(json.dumps({**base, "value": round(wb / (span * 1e3), 2), "unit": "GB/s", "steps": 0, "warmup": 0,

@@ -138,7 +138,7 @@ def test_probe_library_exports(built_lib):
 
     header = (HEADER.parent / "marlin_probe.h").read_text()
     declared = set(re.findall(r"^\s*int\s+(marlin_probe_\w+)\s*\(", header, re.M))
-    assert declared == {"marlin_probe_read", "marlin_probe_empty", "marlin_probe_mfma_32x32x16"}
+    assert declared == {"marlin_probe_read", "marlin_probe_empty", "marlin_probe_mfma_32x32x16", "marlin_probe_smfmac_stream"}
     out = subprocess.run(["nm", "-D", "--defined-only", str(build.PROBE_LIB)], capture_output=True, text=True,
                          check=True).stdout
     assert declared <= set(re.findall(r"\bT\s+(marlin_probe_\w+)", out))

@@ -28,14 +28,15 @@ def _mul(A, wt, C=None):
     return C
 
 
-# (shape, M), grouped by shape so that each 70B weight is built once.  The planner's
-# choices (256 CUs): qkv at M = 512 and o at M = 1024 run 64-row tiles unsplit, o at
-# M = 512 64-row tiles split in two; down splits 128-row tiles four ways at M = 512
-# and two ways at M = 1024; o at M = 4000 has a ragged last 128-row tile; gate_up at
-# M = 4096 is the largest grid (3584 workgroups).
+# (shape, M), grouped by shape so that each 70B weight is built once: every point of
+# the bench's prefill sweep (M in {512, 1024, 2048, 4096}) plus o at M = 4000.  The
+# planner's choices (256 CUs): qkv at M = 512 and o at M = 1024 run 64-row tiles
+# unsplit, o at M = 512 64-row tiles split in two; down splits 128-row tiles four
+# ways at M = 512 and two ways at M = 1024; o at M = 4000 has a ragged last 128-row
+# tile; gate_up at M = 4096 is the largest grid (3584 workgroups).
 PREFILL_CASES = [(name, M) for name in ("qkv", "o", "down", "gate_up")
-                 for M in {"qkv": (512, 1024, 4096), "o": (512, 1024, 4000), "down": (512, 1024, 4096),
-                           "gate_up": (512, 4096)}[name]]
+                 for M in {"qkv": (512, 1024, 2048, 4096), "o": (512, 1024, 2048, 4000, 4096),
+                           "down": (512, 1024, 2048, 4096), "gate_up": (512, 1024, 2048, 4096)}[name]]
 
 
 @pytest.mark.parametrize("name,M", PREFILL_CASES)
