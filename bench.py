@@ -19,7 +19,7 @@ lane-native layout of ``marlin.pack_native``), ``prefill`` (Llama-2-70B shapes, 
 code bytes plus scales), ``floor`` (per decode-sweep call: a plain streaming read of
 its weight bytes and an empty kernel on its planned grid),
 ``stack`` (32 Llama-2-7B layers in sequence, M in {1, 8, 32}; ``stack_native`` runs
-its M = 1 and M = 8 passes on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``copy`` (a plain
+its M = 1 pass on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``copy`` (a plain
 1 GiB device copy: the calibration run for the HBM traffic counters), ``compare``
 (per call site against hipBLASLt dense fp16 and hipSPARSELt 2:4 fp16).
 
@@ -587,7 +587,7 @@ def build_workload(args, device):
             As = {K: synth.make_activation(M, K, synth.SEED_BASE + M, device=device) for _, K, _ in LLAMA7B}
             for l in range(32):
                 for name, K, N in LLAMA7B:
-                    if native and M <= 16:  # what Layer_2_4.to_native() runs
+                    if native and M <= marlin.Layer_2_4.NATIVE_MAX_ROWS:  # what Layer_2_4.to_native() runs
                         calls.append(Call(f"L{l}.{name}", K, N, M, nlayers[l][name], As[K], native_fn))
                         calls[-1].native = True
                     else:
@@ -595,7 +595,8 @@ def build_workload(args, device):
         cfg = {"workload": "decode_stack_32x_llama2_7b" + ("_native" if native else ""), "M": Ms, "layers": 32,
                "groupsize": 128}
         if native:
-            cfg["layout"] = "lane-native for M <= 16 (Layer_2_4.to_native), pack() layout above"
+            cfg["layout"] = (f"lane-native for M <= {marlin.Layer_2_4.NATIVE_MAX_ROWS} (Layer_2_4.to_native), "
+                             "pack() layout above")
     elif wl == "copy":
         n = (1 << 30) // 2
         src = torch.ones(n, dtype=torch.half, device=device)

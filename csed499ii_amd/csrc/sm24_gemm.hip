@@ -341,7 +341,8 @@ __global__ void fill_zero_kernel(uint32_t* p, int n) {
 // once per device with hipGetSymbolAddress; the array's name itself is only a host
 // stand-in.  The first lookup also clears the block with a fill kernel on `stream`
 // (it is zero from module load; the fill is a guard that costs one launch per device
-// and process).
+// and process), unless `stream` is being captured: a fill recorded into the caller's
+// graph would run on every replay, and the block is already zero.
 int get_zeros(int dev, hipStream_t stream, const _Float16** out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   void*& z = g_zeros[dev];
@@ -353,12 +354,14 @@ int get_zeros(int dev, hipStream_t stream, const _Float16** out) {
                 hipGetErrorString(e));
       return MARLIN_HIP_ERR_LAUNCH;
     }
-    hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(64), 0, stream, static_cast<uint32_t*>(p),
-                       (int)(kScratchBytes / 4));
-    const hipError_t le = hipGetLastError();
-    if (le != hipSuccess) {
-      set_error(std::string("marlin_hip: clearing the static scratch failed: ") + hipGetErrorString(le));
-      return MARLIN_HIP_ERR_LAUNCH;
+    if (!capturing(stream)) {
+      hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(64), 0, stream, static_cast<uint32_t*>(p),
+                         (int)(kScratchBytes / 4));
+      const hipError_t le = hipGetLastError();
+      if (le != hipSuccess) {
+        set_error(std::string("marlin_hip: clearing the static scratch failed: ") + hipGetErrorString(le));
+        return MARLIN_HIP_ERR_LAUNCH;
+      }
     }
     z = p;
   }

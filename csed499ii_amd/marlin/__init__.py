@@ -573,7 +573,7 @@ class Layer_2_4(nn.Module):
     def forward(self, A):
         C = torch.empty(A.shape[:-1] + (self.s.shape[1],), dtype=A.dtype, device=A.device)
         A2, C2 = A.view((-1, A.shape[-1])), C.view((-1, C.shape[-1]))
-        if getattr(self, "Bn", None) is not None and A2.shape[0] <= 16 and self.Bn.device == A.device:
+        if getattr(self, "Bn", None) is not None and A2.shape[0] <= self.NATIVE_MAX_ROWS and self.Bn.device == A.device:
             mul_2_4_native(A2, self.Bn, self.metan, C2, self.sn)
             return C
         ws = self.workspace
@@ -582,9 +582,16 @@ class Layer_2_4(nn.Module):
         mul_2_4(A2, self.B, self.meta, C2, self.s, ws)
         return C
 
+    #: Largest batch that ``forward`` runs on the lane-native copy made by
+    #: :meth:`to_native`.  Same box, per call over the decode sweeps: the native kernel
+    #: is faster at 1 row (Llama-2-7B shapes -6.9 %, 70B -5.9 %), level at 2-4 rows,
+    #: and slower from 8 rows (7B at 8 rows +5.0 %, at 16 rows +22.5 % against the
+    #: pack() layout's 16-row kernel).
+    NATIVE_MAX_ROWS = 4
+
     def to_native(self):
         """Keep a lane-native copy of the packed weight (:func:`pack_native`) for
-        batches of at most 16 rows, which ``forward`` then runs on
+        batches of at most ``NATIVE_MAX_ROWS`` rows, which ``forward`` then runs on
         :func:`mul_2_4_native`; larger batches keep using the pack() buffers, which
         stay the module's ``state_dict``.  Needs ``infeatures % 256 == 0``; the copy
         is as large as the packed weight.  ``pack`` and ``load_state_dict`` rebuild

@@ -33,6 +33,12 @@
  * tolerance, a different summation order), and one that needs a larger staging
  * buffer fails with code 3; an eager call of the same shape on the capturing stream
  * before the capture sizes both.
+ * A captured call keeps the scratch of the stream it was captured on, whatever
+ * stream the graph is later replayed on.  So replays of graphs captured on one
+ * stream (torch.cuda.graph() without stream= captures every graph on one default
+ * capture stream) share that stream's scratch with each other and with eager calls
+ * on it: they must not overlap in time.  Graphs captured on distinct streams may be
+ * replayed concurrently.
  */
 #ifndef MARLIN_HIP_H
 #define MARLIN_HIP_H

@@ -179,3 +179,62 @@ def test_spans_hook(built_lib):
                          check=True).stdout
     exported = set(re.findall(r"\bT\s+(marlin_hip_\w+)", out))
     assert set(declared_symbols()) <= exported
+
+
+def _kernel_scratch(lib_path):
+    """{kernel symbol: private segment bytes} of every gfx950 kernel in a HIP shared
+    library: the offload bundles of its .hip_fatbin section, each code object's
+    metadata note read with llvm-readelf."""
+    import struct
+    import tempfile
+
+    readelf = "/opt/rocm/lib/llvm/bin/llvm-readelf"
+    if not pathlib.Path(readelf).exists():
+        pytest.skip("llvm-readelf not available")
+    hdr = subprocess.run([readelf, "-S", "--wide", str(lib_path)], capture_output=True, text=True, check=True).stdout
+    m = re.search(r"\.hip_fatbin\s+PROGBITS\s+[0-9a-f]+\s+([0-9a-f]+)\s+([0-9a-f]+)", hdr)
+    assert m, "no .hip_fatbin section"
+    off, size = int(m.group(1), 16), int(m.group(2), 16)
+    data = pathlib.Path(lib_path).read_bytes()[off:off + size]
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    out, pos = {}, 0
+    while (i := data.find(magic, pos)) >= 0:
+        n = struct.unpack_from("<Q", data, i + 24)[0]
+        p = i + 32
+        for _ in range(n):
+            eo, es, ts = struct.unpack_from("<QQQ", data, p)
+            triple = data[p + 24:p + 24 + ts].decode()
+            p += 24 + ts
+            if "gfx950" not in triple:
+                continue
+            with tempfile.NamedTemporaryFile(suffix=".co") as f:
+                f.write(data[i + eo:i + eo + es])
+                f.flush()
+                notes = subprocess.run([readelf, "--notes", f.name], capture_output=True, text=True,
+                                       check=True).stdout
+            for name, priv in re.findall(r"\.name:\s+(\S+)\n(?:.*\n)*?\s+\.private_segment_fixed_size:\s+(\d+)",
+                                         notes):
+                out[name] = int(priv)
+        pos = i + len(magic)
+    return out
+
+
+def test_no_kernel_spills_to_scratch(built_lib, tmp_path):
+    """No kernel of the GEMM library or of the measurement library keeps anything in
+    scratch (private) memory: a spill would stream every wave's registers through
+    memory.  The reader itself finds the scratch of a kernel built to need it."""
+    from csed499ii_amd import build
+
+    for lib in (_lib.LIB_PATH, build.SPANS_LIB, build.PROBE_LIB):
+        sizes = _kernel_scratch(lib)
+        assert len(sizes) >= (100 if lib != build.PROBE_LIB else 4), lib.name
+        assert not {k: v for k, v in sizes.items() if v}, f"{lib.name}: kernels using scratch"
+    src = tmp_path / "spill.hip"
+    src.write_text("#include <hip/hip_runtime.h>\n"
+                   "__global__ void spill_kernel(const int* i, float* o) {\n"
+                   "  float a[256];\n  for (int k = 0; k < 256; k++) a[k] = o[k] * 2.f;\n"
+                   "  o[threadIdx.x] = a[i[threadIdx.x] & 255];\n}\n")
+    so = tmp_path / "libspill.so"
+    subprocess.run([build.hipcc(), f"--offload-arch={build.ARCH}", "-O3", "-fPIC", "-shared", "-o", str(so),
+                    str(src)], check=True, capture_output=True)
+    assert any(v > 0 for v in _kernel_scratch(so).values())

@@ -142,9 +142,11 @@ def _eager(model, xs):
 
 
 def test_model_graph_matches_oracle_per_layer(model):
-    """One graph holds the three forwards (M = 1 and 8 on the lane-native copies, 32 on
-    the pack() buffers, 384 GEMM calls); three replays equal the eager forward bit for
-    bit, and every linear's output slice equals the oracle on its own input."""
+    """One graph holds the three forwards (M = 1 on the lane-native copies, 8 and 32 on
+    the pack() buffers: Layer_2_4.NATIVE_MAX_ROWS = 4; 384 GEMM calls); three replays
+    equal the eager forward bit for bit, and every linear's output slice equals the
+    oracle on its own input."""
+    assert marlin.Layer_2_4.NATIVE_MAX_ROWS == 4 and MS == (1, 8, 32)
     xs = _inputs()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())

@@ -130,3 +130,63 @@ def test_w3_gemm_bit_exact_against_4bit_path(M, K, N):
     torch.cuda.synchronize()
     assert torch.isfinite(C3).all()
     assert torch.equal(C3, C4)
+
+
+# Shapes that the decode tile table sends to the 8-row batch at 5-8 rows (activations
+# staged through LDS): 4096x4096 on 16-column tiles of 8 waves, 4096x22016 at M = 5 on
+# 32-column tiles, 8192x57344 on 64-column tiles.
+MB8_CASES = [(5, 4096, 4096), (8, 4096, 4096), (5, 4096, 22016), (5, 8192, 57344), (8, 8192, 57344)]
+
+
+@pytest.mark.parametrize("M,K,N", MB8_CASES)
+def test_8row_batch_w3(M, K, N):
+    """3-bit values on the 8-row batch: oracle column slices, and bit-identical to the
+    same values packed at 4 bits."""
+    wt = synth.make_weight(K, N, 11 + K + M, 128, bits=3, device=DEV)
+    A = synth.make_activation(M, K, 13 + M, device=DEV)
+    C3 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    C4 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C3, wt["s"], _ws(N))
+    marlin.mul_2_4(A, _w3_as_w4(wt["B"]), wt["meta"], C4, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    assert torch.equal(C3, C4)
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C3[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"w3 {K}x{N} M={M} slice {c0}")
+
+
+@pytest.mark.parametrize("M,K,N", MB8_CASES)
+def test_8row_batch_meta3(M, K, N):
+    """3-bit metadata on the 8-row batch: bit-identical to the 4-bit metadata call and
+    equal to the oracle on column slices."""
+    wt = synth.make_weight(K, N, 17 + K + M, 128, device=DEV)
+    A = synth.make_activation(M, K, 19 + M, device=DEV)
+    C0 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    C1 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    marlin.mul_2_4(A, wt["B"], wt["meta"], C0, wt["s"], _ws(N))
+    marlin.mul_2_4_meta3(A, wt["B"], marlin.pack_meta3(wt["meta"].reshape(-1)), C1, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    assert torch.equal(C0, C1)
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C1[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"meta3 {K}x{N} M={M} slice {c0}")
+
+
+@pytest.mark.parametrize("M,K,N", MB8_CASES)
+def test_8row_batch_per_column_scales(M, K, N):
+    """Per-column scales (groupsize -1: the scale multiplies the fp16-rounded output)
+    on the 8-row batch, against the oracle on column slices."""
+    wt = synth.make_weight(K, N, 23 + K + M, -1, device=DEV)
+    A = synth.make_activation(M, K, 29 + M, device=DEV)
+    C = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    marlin.mul_2_4(A, wt["B"], wt["meta"], C, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    t = to_cpu(wt)
+    chunks = N // 64
+    for c0 in (0, chunks // 2, chunks - 4):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"g=-1 {K}x{N} M={M} slice {c0}")

@@ -8,8 +8,16 @@ inserts around the MFMA builtins):
 
 * a VALU write of a register that an smfmac reads (A, B, index or accumulator)
   lies at least 2 wait states before it;
-* nothing reads an smfmac's accumulator within 8 wait states after it, except a
-  following smfmac on the same accumulator (hardware-forwarded).
+* nothing reads an smfmac's accumulator within ACC_READ_WAIT_STATES (20) wait states
+  after it, except a following smfmac on the same accumulator (hardware-forwarded).
+
+The window is the CDNA3/CDNA4 ISA's required-independent-instructions rule for an XDL
+(matrix) instruction followed by a VALU, memory or export read of its result
+(NumPasses + 3 wait states, one more on gfx950 for instructions of more than two
+passes; LLVM's GCNHazardRecognizer encodes the table as
+GFX940_XDL_N_PassWriteVgprVALUMemExpReadWaitStates), taken at its largest, 16 passes:
+20 wait states cover every MFMA and smfmac whatever its pass count, so a drain cut
+below that fails here.  The kernels drain 24 (three s_nop 7).
 
 A planted violation is caught (test_checker_catches_planted_hazards), so a pass
 means something.  They also check that the accumulators live in AGPRs and nothing
@@ -27,6 +35,7 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 SRC = ROOT / "csed499ii_amd" / "csrc" / "sm24_prefill.hip"
 DENSE_SRC = ROOT / "csed499ii_amd" / "csrc" / "marlin_dense_prefill.hip"
 MFMA = ("v_smfmac", "v_mfma")
+ACC_READ_WAIT_STATES = 20  # XDL result -> VALU/memory read, 16-pass worst case on gfx950
 
 
 def _regs(tok):
@@ -92,7 +101,7 @@ def hazards(body):
             if pop.startswith("v_") and not pop.startswith(MFMA) and pops and _regs(pops[0]) & reads:
                 found.append(f"VALU write {pw} wait states before smfmac: {ps!r} -> {s!r}")
         dst, w, j = _regs(ops[0]), 0, i + 1
-        while j < len(flat) and w < 8:
+        while j < len(flat) and w < ACC_READ_WAIT_STATES:
             nop, ns, nops = flat[j]
             if nop.startswith(MFMA) and _regs(nops[0]) == dst:
                 break
@@ -134,6 +143,10 @@ def dense_prefill_asm(tmp_path_factory):
 
 
 def test_checker_catches_planted_hazards():
+    """Planted violations are caught: a VALU write one wait state before an smfmac,
+    an accumulator read right after one, and a read after an 8-wait-state drain
+    (enough for a two-pass XDL op, not for the 20 the rule asks of any pass count);
+    a read after the kernels' 24-wait-state drain passes."""
     planted = """
 \tv_pk_mul_f16 v9, v1, v2
 \ts_nop 0
@@ -146,8 +159,11 @@ def test_checker_catches_planted_hazards():
 \tglobal_store_dwordx4 v0, a[16:19], s[0:1]
 """
     found = hazards(planted)
-    assert len(found) == 2, found
+    assert len(found) == 3, found
     assert "1 wait states before" in found[0] and "accumulator read 0" in found[1]
+    assert "accumulator read 8 wait states" in found[2]
+    drained = planted.replace("\ts_nop 7\n", "\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n")
+    assert len(hazards(drained)) == 2
 
 
 def test_prefill_smfmac_hazards(prefill_asm):

@@ -107,3 +107,54 @@ def test_capture_on_fresh_stream_runs_unsplit():
         torch.cuda.synchronize()
         assert torch.equal(C, C_unsplit)
     check_slices(C, A.cpu().numpy(), to_cpu(wt), (0, 170, 340), 4, "captured unsplit gate_up")
+
+
+_FIRST_CALL_CAPTURED = r"""
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from csed499ii_amd import _lib, synth
+lib = _lib.load()
+dev = "cuda:0"
+wt = synth.make_weight(4096, 4096, 331, 128, device=dev)
+A = synth.make_activation(4, 4096, 332, device=dev)
+C = torch.full((4, 4096), float("nan"), dtype=torch.half, device=dev)
+C_eager = torch.empty_like(C)
+torch.cuda.synchronize()
+
+def call(out, stream):
+    err = lib.marlin_hip_mul_2_4_noalloc(
+        ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(wt["B"].data_ptr()), ctypes.c_void_p(wt["meta"].data_ptr()),
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(wt["s"].data_ptr()), 4096, 4, 4096, 64, 0,
+        ctypes.c_void_p(stream.cuda_stream), -1, -1, -1)
+    assert err == 0, _lib.last_error()
+
+s = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):  # the process's first call into the library
+    call(C, s)
+for _ in range(3):
+    C.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    call(C_eager, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert torch.equal(C, C_eager), "replay differs from the eager call"
+print("FIRST_CALL_CAPTURED_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_captured_in_fresh_process():
+    """A process whose very first library call is marlin_hip_mul_2_4_noalloc under
+    stream capture (so the static zero block is looked up while capturing and no
+    clearing launch may be recorded into the graph): replays equal an eager call made
+    afterwards, bit for bit.  Runs in a child process (started, not exec'd)."""
+    import pathlib
+    import subprocess
+    import sys
+
+    root = str(pathlib.Path(__file__).resolve().parents[1])
+    out = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True, text=True,
+                         timeout=110)
+    assert out.returncode == 0 and "FIRST_CALL_CAPTURED_OK" in out.stdout, out.stdout[-2000:] + out.stderr[-2000:]
