@@ -124,27 +124,19 @@ class Call:
 
 
 def kernel_of(c) -> str:
-    """The kernel the library dispatches a call to (the host rules of
-    csed499ii_amd/csrc/sm24_gemm.hip: the prefill kernel, after expanding 3-bit
-    operands to 4 bits, for M >= 17 (N >= 16384 with K >= 8192), 33 (N >= 16384, or
-    N >= 10240 with K >= 8192), 65 (N >= 4096) or 160, with
-    N % 512 == 0 and K % 128 == 0; else the decode kernel up to M = 96 (launches of
-    <= 32 rows); the general kernel beyond; the native kernel for the lane-native
-    layout at M <= 16)."""
+    """The kernel the library dispatches a call to: the lane-native kernel for the
+    lane-native layout, the dense kernels for the dense op, else the first launch's
+    kernel of the library's own plan (``marlin.plan_2_4``: the register-ring decode
+    kernel at 1-8 padded rows, the LDS-DMA decode kernel at 16 and 32, the large-M
+    kernel, or the general one)."""
     if getattr(c, "native", False):
         return "sm24::sm24_native_decode_kernel"
     if getattr(c, "bits", None) == "dense":
         big = c.M >= 65 and c.N % 512 == 0 and c.K % 128 == 0
         return "sm24::marlin_dense_prefill_kernel" if big else "sm24::marlin_dense_kernel"
-    if c.N >= 16384 and c.K >= 8192:
-        min_m = 17
-    else:
-        min_m = 33 if c.N >= 16384 or (c.N >= 10240 and c.K >= 8192) else (65 if c.N >= 4096 else 160)
-    if c.M >= min_m and c.N % 512 == 0 and c.K % 128 == 0:
-        return "sm24::sm24_prefill_kernel"
-    if c.M <= 96:
-        return "sm24::sm24_decode_kernel"
-    return "sm24::sm24_gemm_kernel"
+    kind = marlin.plan_2_4(c.M, c.K, c.N, 128)["kernel"]
+    return {"decode": "sm24::sm24_decode_kernel", "decode_dma": "sm24::sm24_decode_dma_kernel",
+            "large_m": "sm24::sm24_prefill_kernel", "general": "sm24::sm24_gemm_kernel"}[kind]
 
 
 def dense_fn(A, B, meta, C, s, ws):

@@ -803,7 +803,7 @@ int validate(int prob_m, int prob_n, int prob_k, int groupsize, int thread_k, in
 }
 
 
-enum : int { KERNEL_DECODE = 0, KERNEL_PREFILL = 1, KERNEL_GENERAL = 2 };
+enum : int { KERNEL_DECODE = 0, KERNEL_PREFILL = 1, KERNEL_GENERAL = 2, KERNEL_DECODE_DMA = 3 };
 
 // The kernel a call on the reference layout runs (after 3-bit operands at large M are
 // expanded to 4 bits): the decode kernel up to 32 rows, and below the large-M
@@ -817,8 +817,8 @@ int kernel_for(int M, int N, int K) {
 }
 
 // What run() launches for a 4-bit call when nothing limits its scratch:
-// out = {kernel, workgroups of the first launch, threads per workgroup, K splits of
-// the first launch, launches}.
+// out = {kernel (of the first launch), workgroups of the first launch, threads per
+// workgroup, K splits of the first launch, launches}.
 void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
   const int kernel = kernel_for(M, N, K);
   out[0] = kernel;
@@ -826,6 +826,8 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
     const int mc = M < kDecodeMaxM ? M : kDecodeMaxM;
     DecodeShape d = decode_shape(mc, N, K, sms);
     if (noalloc) decode_unsplit(d, K);
+    // the 16- and 32-row batches run the LDS-DMA decode kernel
+    if ((d.mb > decode_batch(mc) ? d.mb : decode_batch(mc)) >= 16) out[0] = KERNEL_DECODE_DMA;
     out[1] = decode_workgroups(N, d);
     out[2] = 64 * d.nw;
     out[3] = d.splits;

@@ -192,7 +192,7 @@ def mul(A, B, C, s, workspace, thread_k=-1, thread_n=-1, sms=-1, max_par=16):
     raise RuntimeError(_lib.last_error() or f"marlin_hip error {err}")
 
 
-_KERNELS = {-1: None, 0: "decode", 1: "large_m", 2: "general"}
+_KERNELS = {-1: None, 0: "decode", 1: "large_m", 2: "general", 3: "decode_dma"}
 
 
 def plan_2_4(M: int, K: int, N: int, groupsize: int = 128, thread_k: int = -1, thread_m: int = -1, sms: int = -1,

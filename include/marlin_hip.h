@@ -84,7 +84,8 @@ int marlin_hip_mul_2_4_noalloc(const void* A, const void* B, const void* meta, v
 
 /* The launch plan of a marlin_hip_mul_2_4 call (noalloc = 0) or of a
  * marlin_hip_mul_2_4_noalloc call (noalloc = 1), computed on the host without a GPU:
- * out[0] kernel (0 decode, 1 large-M, 2 general; -1 for an empty problem),
+ * out[0] kernel of the first launch (0 decode at 1-8 padded rows, 3 decode at 16 or
+ * 32 padded rows (the LDS-DMA kernel), 1 large-M, 2 general; -1 for an empty problem),
  * out[1] workgroups of the first launch, out[2] threads per workgroup, out[3] K
  * splits of the first launch (> 1: the call uses its stream's split-K scratch),
  * out[4] launches.  sms <= 0 plans for 256 compute units.  Returns the codes of

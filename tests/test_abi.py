@@ -98,12 +98,17 @@ def test_plan_without_gpu(built_lib):
     p = marlin.plan_2_4(16, 4096, 22016, sms=256)  # 344 tiles: the 88 past one per CU split in two
     assert p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
     p = marlin.plan_2_4(24, 4096, 22016, sms=256)  # wide N above 16 rows: the 88 tail tiles split in two
-    assert p["kernel"] == "decode" and p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
+    assert p["kernel"] == "decode_dma" and p["splits"] == 2 and p["workgroups"] == 256 + 2 * 88
+    # 1-8 padded rows run the register-ring decode kernel, 16 and 32 the LDS-DMA one
+    # (7B o at 8 rows takes the 8-row batch; 7B qkv at 8 rows the 16-row batch)
+    assert [marlin.plan_2_4(M, 4096, 4096)["kernel"] for M in (1, 4, 8, 9, 16, 32)] == \
+        ["decode"] * 3 + ["decode_dma"] * 3
+    assert marlin.plan_2_4(8, 4096, 12288)["kernel"] == "decode_dma"
     assert marlin.plan_2_4(24, 4096, 22016, noalloc=True)["splits"] == 1
     assert marlin.plan_2_4(4, 8192, 8192)["splits"] == 1  # 16-column tiles fill the CUs
     assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4  # long K, wider N: K split four ways
-    p = marlin.plan_2_4(64, 4096, 4096)  # below the large-M threshold: two decode launches
-    assert p["kernel"] == "decode" and p["launches"] == 2
+    p = marlin.plan_2_4(64, 4096, 4096)  # below the large-M threshold: two decode launches of 32 rows
+    assert p["kernel"] == "decode_dma" and p["launches"] == 2
     for M in (512, 4096):
         p = marlin.plan_2_4(M, 8192, 57344)
         assert p["kernel"] == "large_m" and p["threads"] == 512

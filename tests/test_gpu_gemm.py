@@ -212,7 +212,7 @@ def test_prefill_from_few_rows(M, K, N):
     tile per 512 columns; first, middle and last column slices against the oracle,
     and a repeated call is bit-identical."""
     assert marlin.plan_2_4(M, K, N)["kernel"] == "large_m"
-    assert marlin.plan_2_4(M - 1, K, N)["kernel"] == "decode"
+    assert marlin.plan_2_4(M - 1, K, N)["kernel"] in ("decode", "decode_dma")
     wt, A = _problem(M, N, K, 128, 4100 + M)
     C = _run(wt, A)
     assert torch.isfinite(C).all()
