@@ -795,6 +795,20 @@ def span_row(c, plan, t):
         return round(float(np.max(x)) / 100.0, 3)
 
     clk = float(np.median((c1 - c0) / np.maximum(t3 - t0, 1))) * 100.0 / 1000.0  # GHz
+
+    # the waves that end the call: the latest-ending 1 %, their phases on average
+    end = t3 - t0.min()
+    crit = end >= np.percentile(end, 99)
+
+    def cm(x):
+        return round(float(np.mean(x[crit])) / 100.0, 3)
+
+    # waves per compute unit (word 8: the wave's XCC, shader engine and CU id) and the
+    # median main loop of the waves on CUs of each load
+    cu_ids, cu_inv, cu_waves = np.unique(t[:, 8], return_inverse=True, return_counts=True)
+    load = cu_waves[cu_inv]
+    by_load = {int(v): {"cus": int((cu_waves == v).sum()), "loop_us": med((t2 - t1)[load == v])}
+               for v in np.unique(cu_waves)}
     return {"name": c.name, "M": c.M, "K": c.K, "N": c.N, "workgroups": plan["workgroups"],
             "waves": plan["threads"] // 64,
             "span_us": mx(t3 - t0.min()), "start_spread_us": mx(t0 - t0.min()),
@@ -803,6 +817,9 @@ def span_row(c, plan, t):
             "loop_us": med(t2 - t1), "loop_max_us": mx(t2 - t1),
             "tail_us": med(t3 - t2), "tail_max_us": mx(t3 - t2),
             "wave_us": med(t3 - t0), "clock_GHz": round(clk, 2),
+            "last_waves": {"start_us": cm(t0 - t0.min()), "prologue_us": cm(t1 - t0), "loop_us": cm(t2 - t1),
+                           "tail_us": cm(t3 - t2)},
+            "cus": len(cu_ids), "waves_per_cu": by_load,
             "first_start": int(t0.min()), "last_end": int(t3.max())}
 
 
@@ -860,8 +877,10 @@ def spans_workload(args, device, shapes_70b=False, in_sweep=False):
     median and maximum of the prologue (entry to first loads issued; its median
     split into the wait for the kernel arguments, the load-address setup and the
     issue of the first stages' loads), the main loop (to the last stage's MFMAs) and
-    the reduction and store (to exit).  ``in_sweep``: the same for every call of one
-    pass of the default workload's graph (spans_in_sweep)."""
+    the reduction and store (to exit); the same phases averaged over the waves that
+    end the call (the latest-ending 1 %); and how many waves each compute unit ran,
+    with the median main loop at each load.  ``in_sweep``: the same for every call
+    of one pass of the default workload's graph (spans_in_sweep)."""
     from csed499ii_amd import build as _build
 
     lib = _lib.load()
