@@ -89,6 +89,49 @@ def test_two_streams_split_k_overlap():
     check_slices(C2, A2.cpu().numpy(), t2, (0, 78, 156), 4, "stream 2 qkv M=4")
 
 
+def test_two_graphs_split_k_concurrent_replays():
+    """The scratch rule for graphs: a captured split-K call keeps its capture stream's
+    scratch.  The two split-K layers above, each captured (three calls) on its own
+    capture stream after an eager call there, are replayed back to back on two other
+    streams with no synchronisation between the replays, three rounds with eager work
+    and a synchronisation between them: the graphs never share counters or partials,
+    so every replay equals its eager result bit for bit."""
+    w1 = synth.make_weight(4096, 22016, 501, 128, device=DEV)
+    w2 = synth.make_weight(8192, 10240, 502, 128, device=DEV)
+    A1 = synth.make_activation(24, 4096, 503, device=DEV)
+    A2 = synth.make_activation(4, 8192, 504, device=DEV)
+    cs1, cs2 = torch.cuda.Stream(), torch.cuda.Stream()
+    C1, C2 = torch.empty(24, 22016, dtype=torch.half, device=DEV), torch.empty(4, 10240, dtype=torch.half, device=DEV)
+    eager = []
+    for cs, A, w, C in ((cs1, A1, w1, C1), (cs2, A2, w2, C2)):
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cs):
+            eager.append(_mul(A, w))  # sizes the capture stream's scratch
+    torch.cuda.synchronize()
+    graphs = []
+    for cs, A, w, C in ((cs1, A1, w1, C1), (cs2, A2, w2, C2)):
+        ws = _ws(w["N"])  # allocated (and zeroed) before the capture: nothing but the GEMMs is recorded
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cs):
+            for _ in range(3):
+                marlin.mul_2_4(A, w["B"], w["meta"], C, w["s"], ws)
+        graphs.append((g, ws))
+    rs1, rs2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        C1.fill_(float("nan"))
+        C2.fill_(float("nan"))
+        torch.cuda.synchronize()
+        for _ in range(4):
+            with torch.cuda.stream(rs1):
+                graphs[0][0].replay()
+            with torch.cuda.stream(rs2):
+                graphs[1][0].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C1, eager[0]), "graph 1 (gate_up M=24) differs from its eager result"
+        assert torch.equal(C2, eager[1]), "graph 2 (70B qkv M=4) differs from its eager result"
+
+
 # ---- the reference benchmark's call sites (kernel_bench/bench.py) ----
 
 def _problem_24(m, n, k, groupsize, seed):
