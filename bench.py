@@ -26,7 +26,10 @@ its M = 1 pass on the lane-native layout, as ``Layer_2_4.to_native()`` does), ``
 ``roofline.traffic`` is read from ``profiles/<workload>_hbm_traffic.md`` (HBM
 bytes per launch from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this script,
 scaled by the same counters on the ``copy`` workload); null when that file is
-absent.  ``--eager`` replays the calls without a graph (for counter runs).
+absent.  ``roofline.ceiling`` is the measured ceiling beside the published peak,
+read from the committed profile of ``--workload floor`` / ``floor70b`` (a plain
+streaming read of the same bytes) or ``mfma_floor`` (an MFMA-only stream of the
+same smfmacs), with ``frac`` = achieved / ceiling.  ``--eager`` replays the calls without a graph (for counter runs).
 """
 from __future__ import annotations
 
@@ -624,6 +627,44 @@ def traffic_from_profile(workload: str):
     return None
 
 
+# Measured ceilings beside the published peaks: the profile that records each, the
+# line holding the figure, and the regular expression of the figure in it.
+CEILINGS = {
+    "decode_sweep_llama2_7b": ("decode_floor_llama2_7b.md", "Sum over the 20 calls", r"\(([0-9.]+) GB/s", "GB/s",
+                               "plain streaming read of each call's weight bytes, summed over the sweep "
+                               "(bench.py --workload floor)"),
+    "decode_sweep_llama2_70b": ("decode_floor_llama2_70b.md", "Sum over the 20 calls", r"\(([0-9.]+) GB/s", "GB/s",
+                                "plain streaming read of each call's weight bytes, summed over the sweep "
+                                "(bench.py --workload floor70b)"),
+    "prefill_sweep_llama2_70b": ("prefill_mfma_floor.md", "Sweep: the MFMA-only stream", r"\(([0-9.]+) TFLOP/s",
+                                 "TFLOP/s", "MFMA-only smfmac stream on each call's planned grid with its smfmac "
+                                            "count, summed over the sweep (bench.py --workload mfma_floor)"),
+}
+
+
+def ceiling_from_profile(workload: str, achieved: float):
+    """The measured ceiling of ``workload`` from its committed profile, as
+    {value, unit, frac (achieved / value), source, what}, or None."""
+    import re
+
+    if workload not in CEILINGS:
+        return None
+    fname, key, pat, unit, what = CEILINGS[workload]
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", fname)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key):
+                    m = re.search(pat, line)
+                    if m:
+                        v = float(m.group(1))
+                        return {"value": v, "unit": unit, "frac": round(achieved / v, 4), "source": f"profiles/{fname}",
+                                "what": what}
+    except OSError:
+        return None
+    return None
+
+
 class ProbeRead:
     """The floor workload's stand-in for one decode call: a plain streaming read of the
     call's algorithmic weight bytes (libmarlin_probe.so), each call reading the next
@@ -1101,6 +1142,7 @@ def main():
     roof = roofline_of(wl, res, pass_calls)
     roof["traffic"] = traffic_from_profile(cfg["workload"])
     roof["traffic_unit"] = "bytes per launch"
+    roof["ceiling"] = ceiling_from_profile(cfg["workload"], roof["achieved"])
     value, unit = (res["tflops"], "TFLOP/s") if wl == "prefill" else (res["gbps"], "GB/s")
     out = {**base, "value": round(value, 2), "unit": unit, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": res["ms_per_step"], "config": cfg, "roofline": roof,
@@ -1113,6 +1155,7 @@ def main():
         # 10 steps (~70 ms) after 3 warm-up steps: fewer read ~2 % low from run to run
         pres, pcalls, pcfg = measure(args, "prefill", device, max(10, args.steps // 2), 3)
         proof = roofline_of("prefill", pres, pcalls)
+        proof["ceiling"] = ceiling_from_profile(pcfg["workload"], proof["achieved"])
         out["prefill"] = {"value": round(pres["tflops"], 1), "unit": "TFLOP/s", "steps": pres["steps"],
                           "warmup": pres["warmup"], "ms_per_step": pres["ms_per_step"],
                           "gpu_ms_per_step": pres["gpu_ms_per_step"], "config": pcfg, "roofline": proof}
