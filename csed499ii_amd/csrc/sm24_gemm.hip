@@ -638,19 +638,31 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   } else if (longk) {
     // long K at wide N (the Llama-2-70B shapes): unsplit tiles where N alone fills the
     // CUs (the widest N up to 8 rows), K splits of 64-column tiles otherwise; 32-column
-    // tiles for few rows where N/16 fills one round of two per CU.
+    // tiles for few rows where N/16 fills one round of two per CU.  From forced choices
+    // of TC x NW x S on the four Llama-2-70B shapes at M in {1, 2, 4, 8, 16} (one box):
+    // down 28672x8192 at 2-4 rows two splits of 8-wave tiles (M = 2: 21.9 -> 19.9 us,
+    // M = 4: 21.7 -> 20.5), at 5-8 rows four splits of 4-wave tiles (M = 8: 22.0 ->
+    // 21.2); qkv 8192x10240 at 1-4 rows 32-column tiles (4 waves at M = 1, 8 above)
+    // with the tail split (M = 1: 10.2 -> 10.1, M = 2: 10.9 -> 10.2, M = 4: 11.4 ->
+    // 10.5); at 9-16 rows down two splits of
+    // 8-wave tiles (24.5 -> 24.1), o 8192x8192 one round of 32-column tiles (9.75 ->
+    // 9.25), qkv unsplit 8-wave 64-column tiles (13.5 -> 12.9).
     if (wide32) {
       if (M == 1) d = {32, 8, 1};
       else if (M <= 8) d = {64, M <= 4 ? 4 : 8, 1};
       else d = {64, 4, 2};
-    } else if (M > 8) {
+    } else if (M > 16) {
       d = {64, 4, 4};
+    } else if (M > 8) {
+      if (K >= 16384) d = {64, 8, 2};
+      else if (cus > 0 && (N / 32) % cus == 0) d = {32, 8, 1};
+      else d = {64, 8, 1};
     } else if (K >= 16384) {
-      d = M == 1 ? DecodeShape{64, 8, 2} : M <= 4 ? DecodeShape{64, 4, 4} : DecodeShape{64, 8, 4};
+      d = M <= 4 ? DecodeShape{64, 8, 2} : DecodeShape{64, 4, 4};
     } else if (N / 16 <= 2 * cus) {
       d = {32, 8, 1};
     } else {
-      d = {M <= 4 ? 32 : 64, 4, 4};
+      d = M == 1 ? DecodeShape{32, 4, 1} : M <= 4 ? DecodeShape{32, 8, 1} : DecodeShape{64, 4, 4};
     }
   } else if (M > 16) {
     d = {64, 4, N / 64 >= cus ? 2 : 1};

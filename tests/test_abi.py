@@ -106,7 +106,7 @@ def test_plan_without_gpu(built_lib):
     assert marlin.plan_2_4(8, 4096, 12288)["kernel"] == "decode_dma"
     assert marlin.plan_2_4(24, 4096, 22016, noalloc=True)["splits"] == 1
     assert marlin.plan_2_4(4, 8192, 8192)["splits"] == 1  # 16-column tiles fill the CUs
-    assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4  # long K, wider N: K split four ways
+    assert marlin.plan_2_4(4, 8192, 10240)["splits"] == 4  # long K, wider N: the tail tiles split four ways
     p = marlin.plan_2_4(64, 4096, 4096)  # below the large-M threshold: two decode launches of 32 rows
     assert p["kernel"] == "decode_dma" and p["launches"] == 2
     for M in (512, 4096):
