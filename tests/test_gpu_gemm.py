@@ -147,12 +147,13 @@ def _weight70(K, N):
     return _W70[(K, N)]
 
 
-@pytest.mark.parametrize("M", [1, 4, 7, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 8, 12, 16, 32])
 @pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (28672, 8192), (8192, 57344)])
 def test_decode_llama70b_full_size_slices(K, N, M):
     """The Llama-2-70B decode shapes (long K: 32- and 64-column tiles, K unsplit or
-    split two or four ways; at M = 32 the widest shape, 8192x57344, runs the large-M
-    kernel), checked on column slices; repeated calls must be bit-identical."""
+    split two or four ways, the tail tiles of 8192x10240 split four ways at M <= 4,
+    9-16 rows on the 16-row batch; at M = 32 the widest shape, 8192x57344, runs the
+    large-M kernel), checked on column slices; repeated calls must be bit-identical."""
     wt, t = _weight70(K, N)
     A = synth.make_activation(M, K, 70 + M, device=DEV)
     C = _run(wt, A)
