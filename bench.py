@@ -733,7 +733,8 @@ class SmfmacStream:
     """The mfma_floor workload's stand-in for one prefill call: the MFMA-only stream of
     libmarlin_probe.so on the call's planned grid (workgroups of 8 waves, 128
     accumulator AGPRs each), with as many v_smfmac_f32_32x32x32_f16 per SIMD as the
-    call issues (16 per wave and 64-deep k-step for 128-row tiles, 8 for 64-row)."""
+    call issues per 64-deep k-step: 32 (two waves of 16) for 512x128 tiles, 16 for
+    64-row tiles (two waves of 8) and for the narrow 256x128 tiles (one wave of 16)."""
 
     lib = None
 
@@ -742,9 +743,10 @@ class SmfmacStream:
         self.wbytes, self.kb_bytes, self.flops = 0, 0, c.flops
         self.plan = marlin.plan_2_4(c.M, c.K, c.N, 128)
         tiles = self.plan["workgroups"] // self.plan["splits"]
-        self.rows = 128 if tiles == (c.N // 512) * -(-c.M // 128) else 64
+        self.narrow = self.plan["threads"] == 256
+        self.rows = 128 if self.narrow or tiles == (c.N // 512) * -(-c.M // 128) else 64
         ksteps = -(-(c.K // 64) // self.plan["splits"])
-        self.iters = max(1, ksteps * self.rows // 128)
+        self.iters = max(1, ksteps // 2 if self.narrow else ksteps * self.rows // 128)
         self.dev = torch.device(device).index or 0
         self.out = torch.zeros(self.plan["workgroups"] * 8, dtype=torch.float32, device=device)
         self.clock = torch.zeros(4, dtype=torch.int64, device=device)
@@ -779,6 +781,7 @@ def mfma_floor_workload(args, device, cus=256):
         rounds = -(-st.plan["workgroups"] // cus)
         smf = rounds * st.iters * 32
         rows.append({"name": c.name, "M": c.M, "K": c.K, "N": c.N, "tile_rows": st.rows,
+                     "tile_cols": 256 if st.narrow else 512,
                      "splits": st.plan["splits"], "workgroups": st.plan["workgroups"],
                      "stream_us": su, "stream_TFLOPs": round(c.flops / (su * 1e6), 1),
                      "stream_clock_GHz": round(ghz, 2),

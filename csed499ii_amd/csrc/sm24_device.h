@@ -189,9 +189,11 @@ constexpr int kDecodeMaxM = 32;       // largest batch of one decode launch (two
 constexpr int kDecodeChunkMaxM = 96;  // largest batch run as several decode launches
 constexpr int kPreTileCols = 512;
 constexpr int kPreThreads = 512;  // one wave per 64-column chunk of the tile
-// fp32 partial of one tile of `rows` (128 or 64) batch rows
-constexpr size_t pre_split_bytes(int rows) { return (size_t)512 * rows * sizeof(float); }
-hipError_t launch_prefill(const GemmArgs& a, int rows, bool grouped, hipStream_t stream);
+constexpr int kPreChunks = 8;        // 64-column chunks per tile = waves per workgroup
+constexpr int kPreNarrowChunks = 4;  // the narrow tile: 256 columns (128 rows), 4 waves
+// fp32 partial of one tile of `rows` (128 or 64) batch rows and `chunks` 64-column chunks
+constexpr size_t pre_split_bytes(int rows, int chunks = 8) { return (size_t)64 * chunks * rows * sizeof(float); }
+hipError_t launch_prefill(const GemmArgs& a, int rows, int chunks, bool grouped, hipStream_t stream);
 
 template <int ABID>
 __device__ __forceinline__ float4_t smfmac32(half4_t a, half8_t b, float4_t c, uint32_t idx) {

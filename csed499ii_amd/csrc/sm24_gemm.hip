@@ -468,10 +468,17 @@ __global__ __launch_bounds__(256) void w3_to_w4_kernel(const uint32_t* __restric
 // plus the exchange; it reproduces the measured times of every prefill-sweep call to
 // within ~5 % for both heights and 1-2 splits (forced by MARLIN_HIP_PREFILL_ROWS and
 // MARLIN_HIP_PREFILL_SPLITS, read once).  `nosplit`: one split only.
+// k-step of the narrow tile (4 waves, half the MFMAs of a 512x128 tile's k-step,
+// one wave per SIMD) relative to a 512x128 tile's at the same occupancy, as the
+// planner's model has it when the narrow tile is forced (fitted to forced plans of
+// Llama-2-70B qkv and o at M = 512 and 1024, one box: 0.61-0.71, the higher at low
+// occupancy).
+constexpr double kPreNarrowStep = 0.66;
 struct PrefillPlan {
   int rows;    // batch rows per tile: 128 or 64
   int splits;  // K splits
   int tiles;   // tiles (workgroups per split)
+  int chunks;  // 64-column chunks per tile (= waves): 8, or 4 for the narrow 128-row tile
 };
 // k-step time (us) of a 128-row tile with a fraction x of the CUs busy (measured).
 double prefill_step_us(double x) {
@@ -489,27 +496,47 @@ PrefillPlan prefill_plan(int M, int N, int K, int cus, bool nosplit) {
     return x >= 1 && x <= 16 ? x : 0;
   }();
   static const int forced_rows = env_choice("MARLIN_HIP_PREFILL_ROWS", {64, 128}, 0);
+  static const int forced_chunks = env_choice("MARLIN_HIP_PREFILL_CHUNKS", {kPreNarrowChunks, kPreChunks}, 0);
   const int nks = K / 64;
   const int max_s = nosplit ? 1 : (nks / 8 > 0 ? nks / 8 : 1);  // at least eight k-steps per split
   if (cus < 1) cus = 1;
   const double exchange_bytes_per_us = 5.0e6;
-  PrefillPlan best{128, 1, (N / kPreTileCols) * ((M + 127) / 128)};
+  PrefillPlan best{128, 1, (N / kPreTileCols) * ((M + 127) / 128), kPreChunks};
   double best_cost = 1e30;
-  for (int rows = 128; rows >= 64; rows -= 64) {
-    if (forced_rows && rows != forced_rows) continue;
-    const int tiles = (N / kPreTileCols) * ((M + rows - 1) / rows);
-    if (forced && !nosplit) return PrefillPlan{rows, forced < max_s ? forced : max_s, tiles};
-    const double hscale = rows == 128 ? 1.0 : 0.63;
+  // Candidates: 512-column tiles of 128 or 64 rows (the narrow tile, 256 columns x
+  // 128 rows of 4 waves, only when forced).  A k-step of a 64-row or narrow tile is
+  // a fraction `hscale` of a 512x128 one at the same occupancy.
+  struct Cand {
+    int rows, chunks;
+    double hscale;
+  };
+  const Cand cands[] = {{128, kPreChunks, 1.0}, {64, kPreChunks, 0.63}, {128, kPreNarrowChunks, kPreNarrowStep}};
+  for (const Cand& c : cands) {
+    if ((c.chunks == kPreNarrowChunks) != (forced_chunks == kPreNarrowChunks)) continue;
+    if (forced_rows && c.rows != forced_rows) continue;
+    if (forced_chunks && c.chunks != forced_chunks) continue;
+    const int tiles = (N / (64 * c.chunks)) * ((M + c.rows - 1) / c.rows);
+    if (forced && !nosplit) return PrefillPlan{c.rows, forced < max_s ? forced : max_s, tiles, c.chunks};
     for (int s = 1; s <= 8 && s <= max_s; s++) {
       const long long wgs = (long long)tiles * s, full = wgs / cus, tail = wgs - full * cus;
       double cost = ((double)full * prefill_step_us(1.0) + (tail ? prefill_step_us((double)tail / cus) : 0.0)) *
-                    hscale * nks / s;
-      if (s > 1) cost += 2.0 * tiles * s * (double)pre_split_bytes(rows) / exchange_bytes_per_us;
+                    c.hscale * nks / s;
+      if (s > 1) cost += 2.0 * tiles * s * (double)pre_split_bytes(c.rows, c.chunks) / exchange_bytes_per_us;
       if (cost < 0.98 * best_cost) {
         best_cost = cost;
-        best = PrefillPlan{rows, s, tiles};
+        best = PrefillPlan{c.rows, s, tiles, c.chunks};
       }
     }
+  }
+  // A 64-row plan runs narrow tiles instead where they come to the same count (a
+  // multiple of 128 rows, or the same ragged rounding): the same workgroups, MFMAs and
+  // splits, but every dequantized weight fragment feeds four B fragments instead of
+  // two.  Forced plans of Llama-2-70B (one box): qkv at M = 512 on 160 workgroups
+  // 73.2 -> 66.1 us, o at M = 1024 on 256 89.0 -> 83.2, o at M = 512 in two splits
+  // 58.5 -> 53.7.  MARLIN_HIP_PREFILL_CHUNKS = 8 keeps the 64-row tiles.
+  if (best.rows == 64 && best.chunks == kPreChunks && forced_chunks != kPreChunks) {
+    const int narrow = (N / (64 * kPreNarrowChunks)) * ((M + 127) / 128);
+    if (narrow == best.tiles) best = PrefillPlan{128, best.splits, narrow, kPreNarrowChunks};
   }
   return best;
 }
@@ -847,7 +874,7 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
   } else if (kernel == KERNEL_PREFILL) {
     const PrefillPlan pp = prefill_plan(M, N, K, sms, noalloc || prefill_counters_exceed(N, M));
     out[1] = pp.tiles * pp.splits;
-    out[2] = kPreThreads;
+    out[2] = 64 * pp.chunks;
     out[3] = pp.splits;
     out[4] = 1;
   } else {
@@ -963,7 +990,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
     PrefillPlan pp = prefill_plan(M, N, K, sms, noalloc || prefill_counters_exceed(N, M));
     p.splits = pp.splits;
     if (p.splits > 1) {
-      err = get_scratch(dev, stream, (size_t)pp.tiles * p.splits * pre_split_bytes(pp.rows), &p.counters,
+      err = get_scratch(dev, stream, (size_t)pp.tiles * p.splits * pre_split_bytes(pp.rows, pp.chunks), &p.counters,
                         &p.partial);
       if (err != MARLIN_HIP_OK) return err;
       if (!p.counters) {  // no scratch: the best unsplit plan
@@ -971,7 +998,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
         p.splits = 1;
       }
     }
-    return launch_error(launch_prefill(p, pp.rows, groupsize != -1, stream));
+    return launch_error(launch_prefill(p, pp.rows, pp.chunks, groupsize != -1, stream));
   }
   Plan plan = plan_for(M, N, K, sms);
   const int chunks = N / 64;

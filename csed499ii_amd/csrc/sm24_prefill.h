@@ -46,7 +46,6 @@ struct IntC {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kPreChunks = 8;  // 64-column chunks per tile = waves per workgroup
 static_assert(64 * kPreChunks == kPreTileCols && kPreThreads == 64 * kPreChunks, "tile width");
 constexpr int kPreRing = 4;                        // k-steps resident in LDS
 // Weight side of one k-step, per wave (one chunk): packed values of both k-blocks
@@ -54,18 +53,18 @@ constexpr int kPreRing = 4;                        // k-steps resident in LDS
 // contiguous so that one M0 value serves the wave's weight-side DMAs (instruction
 // offsets 0/1024/1280/1536).
 constexpr int kPreWgtW = 1792;
-constexpr int kPreWgtB = kPreChunks * kPreWgtW;    // weight side of one k-step
 constexpr int kPreActOff = 0;
 // LDS layout of a tile of RG 32-row blocks (128 or 64 batch rows): the activation
 // ring (32 RG rows x 128 bytes per k-step), then the weight ring.
-template <int RG>
+template <int RG, int CT = kPreChunks>
 struct PreLds {
   static constexpr int act_b = 32 * RG * 128;  // activation bytes of one k-step
+  static constexpr int wgt_b = CT * kPreWgtW;   // weight side of one k-step
   static constexpr int wgt_off = kPreActOff + kPreRing * act_b;
-  static constexpr int bytes = wgt_off + kPreRing * kPreWgtB;
+  static constexpr int bytes = wgt_off + kPreRing * wgt_b;
 };
 static_assert(kPreWgtW % 256 == 0, "wave blocks keep the bank pattern");
-static_assert(PreLds<4>::bytes <= 160 * 1024, "LDS");
+static_assert(PreLds<4>::bytes <= 160 * 1024 && PreLds<4, kPreNarrowChunks>::bytes <= 96 * 1024, "LDS");
 
 // v_smfmac_f32_32x32x32_f16 with the accumulator in AGPRs; ABID selects the index
 // halfword.  Written as inline assembly because, for the intrinsic, the compiler
@@ -105,17 +104,19 @@ static_assert(pre_slice0(16, 16) == 14 && pre_slice0(8, 8) == 14, "every slice o
 // tile described above; RG = 2 (64 rows) doubles the tiles of a call for batches whose
 // 128-row tiles leave CUs idle, at twice the dequantization per MFMA (each weight
 // fragment feeds two B fragments instead of four: ~6.5 VALU per MFMA).
-template <bool GROUPED, int RG>
-__global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a) {
+template <bool GROUPED, int RG, int CT>
+__global__ __launch_bounds__(64 * CT, 1) void sm24_prefill_kernel(GemmArgs a) {
   static_assert(RG == 4 || RG == 2, "128- or 64-row tiles");
-  constexpr int MT = 32 * RG, CT = kPreChunks;
+  static_assert(CT == kPreChunks || (CT == kPreNarrowChunks && RG == 4), "512- or (128-row) 256-column tiles");
+  constexpr int MT = 32 * RG;
   constexpr int NF = 2 * RG;               // B fragments per k-step (two k-blocks)
   constexpr int NR = 2 * NF;               // MFMA regions per k-step
-  constexpr int ADMA = RG / 2;             // activation DMA instructions per wave and k-step
+  constexpr int ADMA = 4 * RG / CT;        // activation DMA instructions per wave and k-step
   constexpr int NDMA = ADMA + (GROUPED ? 4 : 3);  // DMA instructions per wave and k-step
-  constexpr int kPreActB = PreLds<RG>::act_b, kPreWgtOff = PreLds<RG>::wgt_off;
-  constexpr int PSTRIDE = 16384 * RG;      // floats of one (tile, split) partial
-  __shared__ __attribute__((aligned(16))) uint8_t lds[PreLds<RG>::bytes];
+  constexpr int kPreActB = PreLds<RG, CT>::act_b, kPreWgtOff = PreLds<RG, CT>::wgt_off;
+  constexpr int kPreWgtB = PreLds<RG, CT>::wgt_b;
+  constexpr int PSTRIDE = 2048 * CT * RG;  // floats of one (tile, split) partial
+  __shared__ __attribute__((aligned(16))) uint8_t lds[PreLds<RG, CT>::bytes];
   typedef __attribute__((address_space(3))) uint8_t lds_u8;
   const uint32_t lbase = (uint32_t)(size_t)(lds_u8*)lds;
 
@@ -167,8 +168,9 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
     const int p = 64 * (ADMA * w + u) + lane, row = p >> 3;
     const int ls = (p & 7) ^ ((row >> 1) & 7);
     const int m = m0 + row < M ? m0 + row : M - 1;
-    // + 1024 (1 - u): instruction u carries offset 1024 u, the base is lowered by 1024
-    act_v[u] = ((uint32_t)m * (uint32_t)K + 8 * ls) * 2 + 1024 * (1 - u);
+    // + 1024 (1 - u % 2): instructions go in pairs, the second of a pair carries
+    // offset 1024, the base is lowered by 1024
+    act_v[u] = ((uint32_t)m * (uint32_t)K + 8 * ls) * 2 + 1024 * (1 - (u & 1));
   }
   // packed values: k-block lane >> 5 of chunk cw; LDS slot s = lane & 31 holds the
   // 16-byte piece 4 g8 + t (words (g8, t, 0..3)) with s = g8 + 8 (t >> 1) + 16 (t & 1),
@@ -198,8 +200,16 @@ __global__ __launch_bounds__(kPreThreads, 1) void sm24_prefill_kernel(GemmArgs a
   auto dma = [&](int s, int q, int g) {
     const uint32_t sc = (uint32_t)(ks0 + s < ks1 ? ks0 + s : ks1 - 1);
     if (g == 0) {
-      if constexpr (ADMA == 2) dma16x2(lbase + kPreActOff + q * kPreActB + 2048 * w, act_v, gA1 + 128 * sc);
-      else dma16x1(lbase + kPreActOff + q * kPreActB + 1024 * w, act_v[0], gA1 + 128 * sc);
+      const uint32_t la = lbase + kPreActOff + q * kPreActB + 1024 * ADMA * w;
+      if constexpr (ADMA == 1) {
+        dma16x1(la, act_v[0], gA1 + 128 * sc);
+      } else {
+#pragma unroll
+        for (int u = 0; u < ADMA; u += 2) {
+          const uint32_t pair[2] = {act_v[u], act_v[u + 1]};
+          dma16x2(la + 1024 * u, pair, gA1 + 128 * sc);
+        }
+      }
     } else {
       const uint32_t l = lbase + kPreWgtOff + q * kPreWgtB + kPreWgtW * w;
       if constexpr (GROUPED)

@@ -168,7 +168,9 @@ def test_checker_catches_planted_hazards():
 
 def test_prefill_smfmac_hazards(prefill_asm):
     kernels = _kernels(prefill_asm)
-    assert len(kernels) == 4  # grouped and per-column scales, 128- and 64-row tiles
+    # grouped and per-column scales: 512-column tiles of 128 and 64 rows (8 waves) and
+    # the narrow 256-column, 128-row tile (4 waves)
+    assert len(kernels) == 6
     for name, body in kernels.items():
         # four unrolled k-steps of 16 (128 rows) or 8 (64 rows) smfmacs
         assert sum(1 for l in body.split("\n") if "v_smfmac" in l) >= (32 if "ELi2E" in name else 64), name
@@ -176,15 +178,21 @@ def test_prefill_smfmac_hazards(prefill_asm):
 
 
 def test_prefill_registers(prefill_asm):
+    # no scratch; 128 (128-row tiles) or 64 (64-row tiles) accumulator registers in
+    # AGPRs; architectural VGPRs (the accumulators' offset in the unified file) at most
+    # 128 for the 8-wave tiles, so that two waves fit on a SIMD, and at most 256 for the
+    # 4-wave narrow tile (one wave per SIMD)
+    seen = 0
     for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", prefill_asm, re.S):
-        body = m.group(2)
-        assert int(re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", body).group(1)) == 0, m.group(1)
-    # 128 (128-row tiles) or 64 (64-row tiles) accumulator registers in AGPRs, and at
-    # most 128 VGPRs, so that two waves fit on a SIMD
-    assert prefill_asm.count("; NumAgprs: 128") == 2
+        name, body = m.group(1), m.group(2)
+        assert int(re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", body).group(1)) == 0, name
+        waves = int(re.search(r"kernelILb[01]ELi\dELi(\d)E", name).group(1))
+        arch = int(re.search(r"\.amdhsa_accum_offset\s+(\d+)", body).group(1))
+        assert arch <= (128 if waves == 8 else 256), (name, arch)
+        seen += 1
+    assert seen == 6
+    assert prefill_asm.count("; NumAgprs: 128") == 4
     assert prefill_asm.count("; NumAgprs: 64") == 2
-    for v in re.findall(r"; NumVgprs: (\d+)", prefill_asm):
-        assert int(v) <= 128
 
 
 def test_dense_prefill_mfma_hazards(dense_prefill_asm):
