@@ -5,7 +5,11 @@
 // v_smfmac_f32_32x32x32_f16 accumulators (128 AGPRs).  K advances in steps of 64 (two
 // 32-deep k-blocks); one k-step is 16 MFMAs per wave.  A second instantiation
 // (template argument RG = 2) runs 64-row tiles: 2 x 2 accumulators (64 AGPRs), 8
-// MFMAs per k-step, for calls whose 128-row tiles would leave CUs idle.
+// MFMAs per k-step, for calls whose 128-row tiles would leave CUs idle.  A third
+// (CT = 4 chunks) runs the narrow tile: 256 columns x 128 rows, 4 waves (one per
+// SIMD, one workgroup per CU by its 92 KiB of LDS), the same per-wave work as the
+// 512-column tile; it replaces 64-row tiles where it comes to the same number of
+// workgroups, so that each dequantized weight fragment still feeds four B fragments.
 //
 // Why two waves per SIMD.  Measured on MI355X (random operands): a 32x32x32 smfmac
 // takes ~35 cycles, and the VALU can issue ~4 instructions of 4 cycles beside it.
