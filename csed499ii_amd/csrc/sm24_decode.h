@@ -244,7 +244,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   // Every slot of every wave holds pieces (the last one repeats its final piece in
   // surplus lanes): loads are never under a branch, so the compiler's waits stay
   // exact.
-  auto slot_live = [&](int) -> bool { return true; };
   // Activation pieces past the last k-block read the zero buffer (an address select:
   // a select on the loaded value would wait for the load right away).
   const uint8_t* zeros = reinterpret_cast<const uint8_t*>(a.zeros);
@@ -318,7 +317,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     // Every LDS operand of the stage is read before the first is used (the larger
     // batches run one or two waves per SIMD, where a read per use exposes its whole
     // latency)
-    constexpr bool HOIST = true;
     uint32_t xr[KP][NCB][2];
     uint32_t x3[KP][NCB][4];  // 3-bit values: the two word pairs of the lane's fields
     // 3-bit metadata: the code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf
@@ -346,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     uint32_t m3y[KP][NCB][2], m3l[KP][NCB][2];
     u32x2 mr[KP][NCB];
     _Float16 sr[NCB];
-    if constexpr (HOIST) {
+    {
 #pragma unroll
       for (int q2 = 0; q2 < KP; q2++) {
         if constexpr (RES) {
@@ -397,18 +395,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
       // columns are never stored, so their operand keeps whatever the register held
       // (LDS reads are paid per active lane).
       half16_t act[RB];
-      if constexpr (!HOIST) {
-        if constexpr (RES) {
-          if (rho < M) {
-            const uint8_t* ap = dyn_lds + o_ract + aoff + 2 * q2 * 64;
-            sact[2 * q2] = *reinterpret_cast<const half8_t*>(ap);
-            sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(ap + 64);
-          }
-        } else if (rho < MB) {
-          sact[2 * q2] = *reinterpret_cast<const half8_t*>(st + o_act + 2 * q2 * MB * 64);
-          sact[2 * q2 + 1] = *reinterpret_cast<const half8_t*>(st + o_act + (2 * q2 + 1) * MB * 64);
-        }
-      }
       act[0] = __builtin_shufflevector(sact[2 * q2], sact[2 * q2 + 1], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14,
                                        15);
 #pragma unroll
@@ -420,9 +406,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         uint32_t lo0, lo1, hi0, hi1;
         if constexpr (VF == VAL4) {
           // words t0 and t0+1 of the lane's k-block row
-          const uint8_t* vp = st + o_val + 2 * q2 * (BPK * 16) + 128 * cb;
-          const uint32_t x0 = (HOIST ? xr[q2][cb][0] : *reinterpret_cast<const uint32_t*>(vp)) >> nsh;
-          const uint32_t x1 = (HOIST ? xr[q2][cb][1] : *reinterpret_cast<const uint32_t*>(vp + 16)) >> nsh;
+          const uint32_t x0 = xr[q2][cb][0] >> nsh;
+          const uint32_t x1 = xr[q2][cb][1] >> nsh;
           lo0 = (x0 & kMask) | kMagic;
           lo1 = (x1 & kMask) | kMagic;
           hi0 = (x0 & kMaskHi) | kMagic;
@@ -431,14 +416,9 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           // 3-bit codes: word w is the 24-bit field at byte 3w of the row, nibble p at
           // bits 3p.  Shifted by 6 blk, the lane's four codes (nibbles 2blk, 2blk+1,
           // 4+2blk, 5+2blk) sit at bits 0, 3, 12, 15.
-          const uint8_t* rowp = st + o_val + 2 * q2 * (BPK * 16);
           const int b0 = 3 * (wi_lane + 32 * cb), b1 = b0 + 12;
-          const uint32_t* p0 = reinterpret_cast<const uint32_t*>(rowp + (b0 & ~3));
-          const uint32_t* p1 = reinterpret_cast<const uint32_t*>(rowp + (b1 & ~3));
-          const uint32_t y0 = __builtin_amdgcn_alignbit(HOIST ? x3[q2][cb][1] : p0[1], HOIST ? x3[q2][cb][0] : p0[0],
-                                                        8 * (b0 & 3) + 6 * blk);
-          const uint32_t y1 = __builtin_amdgcn_alignbit(HOIST ? x3[q2][cb][3] : p1[1], HOIST ? x3[q2][cb][2] : p1[0],
-                                                        8 * (b1 & 3) + 6 * blk);
+          const uint32_t y0 = __builtin_amdgcn_alignbit(x3[q2][cb][1], x3[q2][cb][0], 8 * (b0 & 3) + 6 * blk);
+          const uint32_t y1 = __builtin_amdgcn_alignbit(x3[q2][cb][3], x3[q2][cb][2], 8 * (b1 & 3) + 6 * blk);
           // One shift and one bit-field insert move the codes at bits 12 and 15 up to
           // 16 and 19, so that each half pair's codes sit 16 bits apart: masked and
           // or-ed with the magic exponent they are the halves 1024 + c (bits 0 / 16)
@@ -467,8 +447,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
         // unit 16*jb + 2*gt + jj
         uint32_t idx;
         if constexpr (MF == META4) {
-          const u32x2 unit =
-              HOIST ? mr[q2][cb] : *reinterpret_cast<const u32x2*>(st + o_meta + 2 * q2 * (MPK * 16) + 32 * cb);
+          const u32x2 unit = mr[q2][cb];
           idx = __builtin_amdgcn_perm(unit.y, unit.x, msel);
         } else {
           // 3-bit code word of metadata word u = 32*jb + 4*g + 2*jj + ehalf: the low
@@ -480,14 +459,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           uint32_t v[2];
 #pragma unroll
           for (int ehalf = 0; ehalf < 2; ehalf++) {
-            uint32_t Y, L;
-            if constexpr (HOIST) {
-              Y = m3y[q2][cb][ehalf];
-              L = m3l[q2][cb][ehalf];
-            } else {
-              m3_read(st, q2, cb, ehalf, Y, L);
-            }
-            v[ehalf] = __builtin_amdgcn_alignbit(Y, L, m3_shift(cb) & 31u);
+            v[ehalf] = __builtin_amdgcn_alignbit(m3y[q2][cb][ehalf], m3l[q2][cb][ehalf], m3_shift(cb) & 31u);
           }
           // selector bytes {ca0, ca1, cb0, cb1} (code a / b of ehalf 0 / 1): the low
           // bytes of v[0], v[1] side by side, their b codes moved up by 13 bits
@@ -497,7 +469,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
           idx = (nib & 0x0f0fu) | ((nib >> 12) & 0xf0f0u);                 // byte e: a | b << 4 of ehalf e
         }
         if constexpr (GROUPED) {
-          const _Float16 sc = HOIST ? sr[cb] : *reinterpret_cast<const _Float16*>(st + o_scale + 32 * cb);
+          const _Float16 sc = sr[cb];
           aop = aop * (half8_t){sc, sc, sc, sc, sc, sc, sc, sc};
         }
 #pragma unroll
@@ -523,7 +495,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
   for (int i = 0; i < D; i++) {
 #pragma unroll
     for (int q = 0; q < SL; q++)
-      if (slot_live(q)) ring[i][q] = load_slot(q, i);
+      ring[i][q] = load_slot(q, i);
     __builtin_amdgcn_sched_barrier(0);
   }
   if constexpr (RES) {
@@ -538,10 +510,8 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
     uint8_t* st = wlds + (i & 1) * STAGE;
 #pragma unroll
     for (int q = 0; q < SL; q++) {
-      if (slot_live(q)) {
-        *reinterpret_cast<u32x4*>(st + slds[q]) = ring[i][q];
-        if (reload) ring[i][q] = load_slot(q, s + D);
-      }
+      *reinterpret_cast<u32x4*>(st + slds[q]) = ring[i][q];
+      if (reload) ring[i][q] = load_slot(q, s + D);
     }
     __builtin_amdgcn_sched_barrier(0);
     compute(st, (uint32_t)s * (KS * 64));
