@@ -47,8 +47,15 @@ def compile_flags() -> list[str]:
     ]
 
 
-# Per-source extra flags (none at present).
-EXTRA_FLAGS: dict[str, list[str]] = {}
+# The translation units of the decode-sized kernels (sm24_decode_*, the lane-native
+# decode kernel in sm24_gemm.hip, the dense Marlin kernel): their leading scalar
+# arguments (up to 14 dwords) are preloaded into SGPRs by the dispatcher, so their
+# prologue waits for no kernel-argument load.  Kernels whose first argument is a
+# struct are not affected.
+_PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
+EXTRA_FLAGS: dict[str, list[str]] = {
+    name: _PRELOAD for name in ("sm24_decode_16.hip", "sm24_decode_32.hip", "sm24_decode_64.hip", "sm24_gemm.hip",
+                                "marlin_dense.hip")}
 
 # hipcc's host pass does not know the packed-fp32 target feature: drop that noise.
 _NOISE = ("packed-fp32-ops", "is not a recognized feature")

@@ -58,8 +58,22 @@ struct DenseFrag {
   half8_t act[BB];   // activation B operands
 };
 
+// The fields the prologue needs first come as leading scalar arguments, preloaded
+// into SGPRs (this translation unit is built with -mllvm
+// -amdgpu-kernarg-preload-count=14), ahead of the whole DenseArgs.
 template <int BB, int NW, bool GROUPED>
-__global__ __launch_bounds__(64 * NW) void marlin_dense_kernel(DenseArgs a) {
+__global__ __launch_bounds__(64 * NW) void marlin_dense_kernel(const _Float16* A_, const uint32_t* B_,
+                                                               const _Float16* s_, const _Float16* zeros_, int M_,
+                                                               int N_, int K_, int splits_, DenseArgs a_) {
+  DenseArgs a = a_;
+  a.A = A_;
+  a.B = B_;
+  a.s = s_;
+  a.zeros = zeros_;
+  a.M = M_;
+  a.N = N_;
+  a.K = K_;
+  a.splits = splits_;
   constexpr int NT = 64 * NW;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -280,7 +294,8 @@ int dense_validate(int prob_m, int prob_n, int prob_k, int groupsize, int thread
 template <int BB, bool G>
 hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t stream) {
   constexpr int NW = 4;
-  hipLaunchKernelGGL((marlin_dense_kernel<BB, NW, G>), grid, dim3(64 * NW), 0, stream, a);
+  hipLaunchKernelGGL((marlin_dense_kernel<BB, NW, G>), grid, dim3(64 * NW), 0, stream, a.A, a.B, a.s, a.zeros, a.M,
+                     a.N, a.K, a.splits, a);
   return hipGetLastError();
 }
 

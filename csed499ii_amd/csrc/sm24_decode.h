@@ -46,8 +46,10 @@ constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP, bool RES>
-__global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
-  constexpr int NT = 64 * NW;                           // threads
+__global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, const void* meta_, const _Float16* s_,
+                                                              const _Float16* A_, const _Float16* zeros_, int M_,
+                                                              int N_, int K_, int splits_, GemmArgs a_) {
+  const GemmArgs a = with_lead(a_, B_, meta_, s_, A_, zeros_, M_, N_, K_, splits_);
   constexpr int NCB = TC / 16;                          // 16-column MFMA blocks per tile
   constexpr int KPW = cmax(2, 64 / TC);                 // k-blocks per wave per stage (pairs)
   constexpr int KS = KPW * NW;                          // k-blocks per stage
@@ -399,7 +401,6 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(GemmArgs a) {
                                        15);
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
-        const int gt = 2 * cb + gl;
         // values: bytes blk, blk+2 of words t0, t0+1; low nibbles -> groups t0, t0+1,
         // high nibbles (16x) -> groups t0+4, t0+5, each {slot 0, slot 1}; as halves
         // 1024 + q (lo) and 1024 + 16q (hi) by the magic-number trick

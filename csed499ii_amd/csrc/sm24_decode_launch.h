@@ -40,7 +40,8 @@ void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
     // pieces travel with each stage into LDS; against the register-ring kernel with
     // direct activation operands (same tile table, same box): Llama-2-7B at M = 16 qkv
     // 8.37 -> 7.71, o 6.54 -> 5.88, gate_up 12.21 -> 11.35, down 9.30 -> 8.71 us.
-    hipLaunchKernelGGL((sm24_decode_dma_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sm24_decode_dma_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP>), grid, block, 0, stream,
+                       a.B, a.meta, a.s, a.A, a.zeros, a.M, a.N, a.K, a.splits, a);
   } else {
     static const int forced_res = env_choice("MARLIN_HIP_DECODE_RES", {0, 1}, 1);
     constexpr int ks = NW * (64 / TC > 2 ? 64 / TC : 2);
@@ -52,10 +53,12 @@ void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
     const bool fits = stat <= kCuLds && dyn <= kCuLds - stat &&
                       (stat + dyn <= kDecodeLdsMax || (cus > 0 && grid.x <= (unsigned)cus));
     if (forced_res == 1 && nst_max >= 8 && fits) {
-      hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>), grid, block, dyn, stream, a);
+      hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>), grid, block, dyn, stream,
+                         a.B, a.meta, a.s, a.A, a.zeros, a.M, a.N, a.K, a.splits, a);
       return;
     }
-    hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream,
+                       a.B, a.meta, a.s, a.A, a.zeros, a.M, a.N, a.K, a.splits, a);
   }
 }
 

@@ -124,6 +124,26 @@ struct GemmArgs {
   uint64_t* spans;     // per-wave timestamps (only read by a build with SM24_SPANS=1)
 };
 
+// The decode kernels take the fields their prologue needs first (14 dwords) as
+// leading scalar arguments ahead of the whole GemmArgs: the translation units that
+// instantiate them are built with -mllvm -amdgpu-kernarg-preload-count=14, so
+// gfx950's dispatcher preloads those fields into SGPRs and the first address
+// computation waits for no kernel-argument load.
+__device__ __forceinline__ GemmArgs with_lead(GemmArgs a, const void* B, const void* meta, const _Float16* s,
+                                              const _Float16* A, const _Float16* zeros, int M, int N, int K,
+                                              int splits) {
+  a.B = B;
+  a.meta = meta;
+  a.s = s;
+  a.A = A;
+  a.zeros = zeros;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.splits = splits;
+  return a;
+}
+
 // Per-wave phase timestamps of the decode kernel, compiled in only by the
 // measurement build (SM24_SPANS=1, libmarlin_hip_spans.so): wave w of workgroup b
 // writes kSpanWords 64-bit words at spans[(b * waves + w) * kSpanWords]: the 100 MHz

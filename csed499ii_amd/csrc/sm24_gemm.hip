@@ -1138,7 +1138,8 @@ template <int MB, int NCB, bool G>
 void launch_native_t(const NativeArgs& a, size_t lds, hipStream_t stream) {
   constexpr int D = NCB == 1 ? 4 : 2;
   hipLaunchKernelGGL((sm24_native_decode_kernel<MB, NCB, 4, D, G>),
-                     dim3((unsigned)(a.N / (16 * NCB)), (unsigned)a.splits), dim3(256), lds, stream, a);
+                     dim3((unsigned)(a.N / (16 * NCB)), (unsigned)a.splits), dim3(256), lds, stream, a.A, a.W, a.X,
+                     a.S, a.s_col, a.M, a.N, a.K, a.splits, a);
 }
 
 int run_native(const void* A, const void* W, const void* X, void* C, const void* S, int N, int M, int K,

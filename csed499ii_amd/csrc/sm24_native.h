@@ -171,8 +171,24 @@ __global__ __launch_bounds__(256) void native_unpack_meta_kernel(const u32x2* __
 // waves never wait on each other until the end.  Each quad is 4 smfmacs per block
 // into 4 accumulators.  At the end the NW partial tiles are added in LDS in wave
 // order (deterministic), and with split-K handed off as in the decode kernel.
+// The fields the prologue needs first come as leading scalar arguments, preloaded
+// into SGPRs (the translation unit is built with -mllvm
+// -amdgpu-kernarg-preload-count=14), ahead of the whole NativeArgs.
 template <int MB, int NCB, int NW, int D, bool GROUPED>
-__global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(NativeArgs a) {
+__global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(const _Float16* A_, const u32x4* W_,
+                                                                     const u32x2* X_, const uint32_t* S_,
+                                                                     const _Float16* s_col_, int M_, int N_, int K_,
+                                                                     int splits_, NativeArgs a_) {
+  NativeArgs a = a_;
+  a.A = A_;
+  a.W = W_;
+  a.X = X_;
+  a.S = S_;
+  a.s_col = s_col_;
+  a.M = M_;
+  a.N = N_;
+  a.K = K_;
+  a.splits = splits_;
   extern __shared__ __attribute__((aligned(16))) uint8_t nlds[];
   constexpr int NT = 64 * NW;
   const int tid = threadIdx.x, lane = tid & 63;
