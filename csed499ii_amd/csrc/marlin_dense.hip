@@ -60,16 +60,17 @@ struct DenseFrag {
 
 // The fields the prologue needs first come as leading scalar arguments, preloaded
 // into SGPRs (this translation unit is built with -mllvm
-// -amdgpu-kernarg-preload-count=14), ahead of the whole DenseArgs.
+// -amdgpu-kernarg-preload-count=14), ahead of the whole DenseArgs; the fp16
+// pointers travel as void pointers, which keeps the kernel's name demangleable.
 template <int BB, int NW, bool GROUPED>
-__global__ __launch_bounds__(64 * NW) void marlin_dense_kernel(const _Float16* A_, const uint32_t* B_,
-                                                               const _Float16* s_, const _Float16* zeros_, int M_,
-                                                               int N_, int K_, int splits_, DenseArgs a_) {
+__global__ __launch_bounds__(64 * NW) void marlin_dense_kernel(const void* A_, const uint32_t* B_, const void* s_,
+                                                               const void* zeros_, int M_, int N_, int K_, int splits_,
+                                                               DenseArgs a_) {
   DenseArgs a = a_;
-  a.A = A_;
+  a.A = static_cast<const _Float16*>(A_);
   a.B = B_;
-  a.s = s_;
-  a.zeros = zeros_;
+  a.s = static_cast<const _Float16*>(s_);
+  a.zeros = static_cast<const _Float16*>(zeros_);
   a.M = M_;
   a.N = N_;
   a.K = K_;

@@ -93,9 +93,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
-__global__ __launch_bounds__(64 * NW) void sm24_decode_dma_kernel(const void* B_, const void* meta_, const _Float16* s_,
-                                                                  const _Float16* A_, const _Float16* zeros_, int M_,
-                                                                  int N_, int K_, int splits_, GemmArgs a_) {
+__global__ __launch_bounds__(64 * NW) void sm24_decode_dma_kernel(const void* B_, const void* meta_, const void* s_,
+                                                                  const void* A_, const void* zeros_, int M_, int N_,
+                                                                  int K_, int splits_, GemmArgs a_) {
   const GemmArgs a = with_lead(a_, B_, meta_, s_, A_, zeros_, M_, N_, K_, splits_);
   constexpr int NCB = TC / 16;                           // 16-column MFMA blocks per tile
   constexpr int KPW = cmax(2, 64 / TC);                  // k-blocks per wave per stage (pairs)

@@ -128,15 +128,16 @@ struct GemmArgs {
 // leading scalar arguments ahead of the whole GemmArgs: the translation units that
 // instantiate them are built with -mllvm -amdgpu-kernarg-preload-count=14, so
 // gfx950's dispatcher preloads those fields into SGPRs and the first address
-// computation waits for no kernel-argument load.
-__device__ __forceinline__ GemmArgs with_lead(GemmArgs a, const void* B, const void* meta, const _Float16* s,
-                                              const _Float16* A, const _Float16* zeros, int M, int N, int K,
-                                              int splits) {
+// computation waits for no kernel-argument load.  (The fp16 pointers travel as void
+// pointers: a _Float16 in a kernel's signature leaves its name undemangled in the
+// profilers' traces.)
+__device__ __forceinline__ GemmArgs with_lead(GemmArgs a, const void* B, const void* meta, const void* s,
+                                              const void* A, const void* zeros, int M, int N, int K, int splits) {
   a.B = B;
   a.meta = meta;
-  a.s = s;
-  a.A = A;
-  a.zeros = zeros;
+  a.s = static_cast<const _Float16*>(s);
+  a.A = static_cast<const _Float16*>(A);
+  a.zeros = static_cast<const _Float16*>(zeros);
   a.M = M;
   a.N = N;
   a.K = K;

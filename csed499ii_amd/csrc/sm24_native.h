@@ -173,18 +173,18 @@ __global__ __launch_bounds__(256) void native_unpack_meta_kernel(const u32x2* __
 // order (deterministic), and with split-K handed off as in the decode kernel.
 // The fields the prologue needs first come as leading scalar arguments, preloaded
 // into SGPRs (the translation unit is built with -mllvm
-// -amdgpu-kernarg-preload-count=14), ahead of the whole NativeArgs.
+// -amdgpu-kernarg-preload-count=14), ahead of the whole NativeArgs; the fp16
+// pointers travel as void pointers, which keeps the kernel's name demangleable.
 template <int MB, int NCB, int NW, int D, bool GROUPED>
-__global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(const _Float16* A_, const u32x4* W_,
-                                                                     const u32x2* X_, const uint32_t* S_,
-                                                                     const _Float16* s_col_, int M_, int N_, int K_,
-                                                                     int splits_, NativeArgs a_) {
+__global__ __launch_bounds__(64 * NW) void sm24_native_decode_kernel(const void* A_, const u32x4* W_, const u32x2* X_,
+                                                                     const uint32_t* S_, const void* s_col_, int M_,
+                                                                     int N_, int K_, int splits_, NativeArgs a_) {
   NativeArgs a = a_;
-  a.A = A_;
+  a.A = static_cast<const _Float16*>(A_);
   a.W = W_;
   a.X = X_;
   a.S = S_;
-  a.s_col = s_col_;
+  a.s_col = static_cast<const _Float16*>(s_col_);
   a.M = M_;
   a.N = N_;
   a.K = K_;
