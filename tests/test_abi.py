@@ -186,23 +186,23 @@ def test_spans_hook(built_lib):
     assert set(declared_symbols()) <= exported
 
 
-def _kernel_scratch(lib_path):
-    """{kernel symbol: private segment bytes} of every gfx950 kernel in a HIP shared
-    library: the offload bundles of its .hip_fatbin section, each code object's
-    metadata note read with llvm-readelf."""
-    import struct
-    import tempfile
+READELF = "/opt/rocm/lib/llvm/bin/llvm-readelf"
 
-    readelf = "/opt/rocm/lib/llvm/bin/llvm-readelf"
-    if not pathlib.Path(readelf).exists():
+
+def _code_objects(lib_path):
+    """The gfx950 code objects (bytes) in the offload bundles of a HIP shared
+    library's .hip_fatbin section."""
+    import struct
+
+    if not pathlib.Path(READELF).exists():
         pytest.skip("llvm-readelf not available")
-    hdr = subprocess.run([readelf, "-S", "--wide", str(lib_path)], capture_output=True, text=True, check=True).stdout
+    hdr = subprocess.run([READELF, "-S", "--wide", str(lib_path)], capture_output=True, text=True, check=True).stdout
     m = re.search(r"\.hip_fatbin\s+PROGBITS\s+[0-9a-f]+\s+([0-9a-f]+)\s+([0-9a-f]+)", hdr)
     assert m, "no .hip_fatbin section"
     off, size = int(m.group(1), 16), int(m.group(2), 16)
     data = pathlib.Path(lib_path).read_bytes()[off:off + size]
     magic = b"__CLANG_OFFLOAD_BUNDLE__"
-    out, pos = {}, 0
+    pos = 0
     while (i := data.find(magic, pos)) >= 0:
         n = struct.unpack_from("<Q", data, i + 24)[0]
         p = i + 32
@@ -210,18 +210,65 @@ def _kernel_scratch(lib_path):
             eo, es, ts = struct.unpack_from("<QQQ", data, p)
             triple = data[p + 24:p + 24 + ts].decode()
             p += 24 + ts
-            if "gfx950" not in triple:
-                continue
-            with tempfile.NamedTemporaryFile(suffix=".co") as f:
-                f.write(data[i + eo:i + eo + es])
-                f.flush()
-                notes = subprocess.run([readelf, "--notes", f.name], capture_output=True, text=True,
-                                       check=True).stdout
-            for name, priv in re.findall(r"\.name:\s+(\S+)\n(?:.*\n)*?\s+\.private_segment_fixed_size:\s+(\d+)",
-                                         notes):
-                out[name] = int(priv)
+            if "gfx950" in triple:
+                yield data[i + eo:i + eo + es]
         pos = i + len(magic)
+
+
+def _kernel_scratch(lib_path):
+    """{kernel symbol: private segment bytes} of every gfx950 kernel in a HIP shared
+    library: each code object's metadata note read with llvm-readelf."""
+    import tempfile
+
+    out = {}
+    for co in _code_objects(lib_path):
+        with tempfile.NamedTemporaryFile(suffix=".co") as f:
+            f.write(co)
+            f.flush()
+            notes = subprocess.run([READELF, "--notes", f.name], capture_output=True, text=True, check=True).stdout
+        for name, priv in re.findall(r"\.name:\s+(\S+)\n(?:.*\n)*?\s+\.private_segment_fixed_size:\s+(\d+)",
+                                     notes):
+            out[name] = int(priv)
     return out
+
+
+def _kernarg_preload(lib_path):
+    """{kernel symbol: kernel-argument dwords preloaded into SGPRs} of every gfx950
+    kernel of a HIP shared library, from its kernel descriptor (the 64-byte `.kd`
+    object: uint16 at byte 58, bits 0-6 KERNARG_PRELOAD_SPEC_LENGTH)."""
+    import struct
+    import tempfile
+
+    out = {}
+    for co in _code_objects(lib_path):
+        with tempfile.NamedTemporaryFile(suffix=".co") as f:
+            f.write(co)
+            f.flush()
+            secs = subprocess.run([READELF, "-S", "--wide", f.name], capture_output=True, text=True, check=True).stdout
+            syms = subprocess.run([READELF, "-s", "--wide", f.name], capture_output=True, text=True, check=True).stdout
+        # [Nr] Name Type Address Off Size ...: address ranges mapped to file offsets
+        ranges = [(int(a, 16), int(o, 16), int(z, 16))
+                  for a, o, z in re.findall(r"\]\s+\S+\s+\S+\s+([0-9a-f]{8,})\s+([0-9a-f]{6,})\s+([0-9a-f]{6,})", secs)]
+        for value, name in re.findall(r"^\s*\d+:\s+([0-9a-f]+)\s+64\s+OBJECT\s+\S+\s+\S+\s+\S+\s+(\S+)\.kd$", syms,
+                                      re.M):
+            addr = int(value, 16)
+            base = next(o + addr - a for a, o, z in ranges if a <= addr < a + z)
+            out[name] = struct.unpack_from("<H", co, base + 58)[0] & 0x7F
+    return out
+
+
+def test_decode_kernels_preload_their_leading_arguments(built_lib):
+    """The decode-sized kernels take the fields their prologue needs first as leading
+    scalar arguments, built to be preloaded into SGPRs: the register-ring, LDS-DMA
+    and lane-native decode kernels 14 dwords, the dense Marlin kernel 12; kernels whose
+    first argument is a struct preload nothing."""
+    pre = _kernarg_preload(_lib.LIB_PATH)
+    fam = {"sm24_decode_kernel": 14, "sm24_decode_dma_kernel": 14, "sm24_native_decode_kernel": 14,
+           "marlin_dense_kernel": 12, "sm24_prefill_kernel": 0}
+    for part, want in fam.items():
+        got = {k: v for k, v in pre.items() if part + "I" in k}
+        assert got, part
+        assert set(got.values()) == {want}, (part, sorted(set(got.values())))
 
 
 def test_no_kernel_spills_to_scratch(built_lib, tmp_path):
