@@ -698,7 +698,11 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   } else if (wide32) {
     d = {32, 4, 1};
   } else {
-    d = {16, 4, 1};
+    // 3-4 rows (the padded batch of 4) on 64-column tiles of 8 waves, as 5-8 rows,
+    // where those tiles fill three quarters of the CUs: 7B qkv 4096x12288 at M = 4
+    // 7.47 / 7.39 -> 7.14 us (forced sweep, one box); at 1-2 rows the 16-column tiles
+    // stay faster (M = 2: 6.83 against 7.09 us)
+    d = M >= 3 && 4 * (N / 64) >= 3 * cus ? DecodeShape{64, 8, 1} : DecodeShape{16, 4, 1};
   }
   if (mid && d.mb == 0) d.mb = 16;  // the rest keep the 16-row batch
   if (forced_tc) d.tc = forced_tc;
