@@ -45,8 +45,11 @@ namespace sm24 {
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
-template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP, bool RES>
-__global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, const void* meta_, const void* s_,
+// G: tiles per workgroup, each on its own NW waves, sharing the workgroup's resident
+// activation rows (G = 3 for 16-column tiles, unsplit: one workgroup per CU where
+// three tiles per CU would otherwise be three workgroups copying the same rows).
+template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP, bool RES, int G = 1>
+__global__ __launch_bounds__(64 * NW * G) void sm24_decode_kernel(const void* B_, const void* meta_, const void* s_,
                                                               const void* A_, const void* zeros_, int M_, int N_,
                                                               int K_, int splits_, GemmArgs a_) {
   const GemmArgs a = with_lead(a_, B_, meta_, s_, A_, zeros_, M_, N_, K_, splits_);
@@ -91,14 +94,17 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
   // reduction.
   constexpr int REDP = TC + 4;
   constexpr int REDB = NW * 16 * REDP * 4;
-  constexpr int LDSB = 2 * NW * STAGE > REDB ? 2 * NW * STAGE : REDB;
+  static_assert(G == 1 || (G == 3 && TC == 16), "three 16-column tiles per workgroup, or one tile");
+  constexpr int LDSB = 2 * NW * G * STAGE > G * REDB ? 2 * NW * G * STAGE : G * REDB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDSB];
 
   SpanStamps sp;  // phase timestamps (measurement build only)
   sp.mark(0);
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = G == 1 ? 0 : wall / NW;     // this wave's tile of the workgroup
+  const int wave = G == 1 ? wall : wall % NW;  // its wave among that tile's NW
+  const int tid = threadIdx.x - 64 * NW * grp;  // its thread among that tile's
   const int N = a.N, K = a.K, M = a.M;
   sp.mark_args(N);
   const int nkb = K >> 5;
@@ -117,7 +123,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
   int z = 0, st0 = 0, nst = nst_all;  // split z covers stages [st0, st0 + nst)
   int tile = blockIdx.x;
   int ptile = 0;                      // index of the tile among the split tiles
-  if (a.splits > 1) {  // uniform; nst_all * S is small, so 32 bits are exact
+  if (G == 1 && a.splits > 1) {  // uniform; nst_all * S is small, so 32 bits are exact
     const int T0 = a.tail_from;
     if (T0 == 0) {
       S = a.splits;
@@ -142,7 +148,13 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
   // values are whole lines), so they go to blocks b = 8*(SUB*q + s) + x, which all
   // sit on XCD x: each line is fetched from HBM once instead of once per tile.
   constexpr int SUB = 64 / TC;
-  if constexpr (SUB > 1) {
+  if constexpr (G > 1) {
+    // block b = 8 j + x (on XCD x) runs tiles k = G j + grp of XCD x's share: chunk
+    // 8 (k / SUB) + x, its tile k % SUB (the host launches ntiles / G blocks, unsplit,
+    // with ntiles a multiple of 8 SUB G)
+    const int x = blockIdx.x & 7, k = G * (blockIdx.x >> 3) + grp;
+    tile = (8 * (k / SUB) + x) * SUB + k % SUB;
+  } else if constexpr (SUB > 1) {
     if (ntiles % (8 * SUB) == 0) {
       const int x = tile & 7, jx = tile >> 3;
       tile = (8 * (jx / SUB) + x) * SUB + jx % SUB;
@@ -167,7 +179,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
 #pragma unroll
     for (int m = 0; m < MB; m++) {
       if (m < M) {  // uniform
-        for (int jc = wave; jc < cpr; jc += NW) {
+        for (int jc = wall; jc < cpr; jc += NW * G) {
           const uint32_t b = (uint32_t)jc * 1024u + 16u * lane;
           if (b < span) {
             const int k = k0 + (int)(b >> 1);
@@ -506,7 +518,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
     __syncthreads();
   }
   sp.mark(3);
-  uint8_t* const wlds = lds + wave * 2 * STAGE;  // this wave's two stage buffers
+  uint8_t* const wlds = lds + wall * 2 * STAGE;  // this wave's two stage buffers
   auto stage = [&](int i, bool reload, int s) {
     uint8_t* st = wlds + (i & 1) * STAGE;
 #pragma unroll
@@ -539,7 +551,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
   // partial tile, then thread t < 4*TC adds the NW partials of 4 columns of one row in
   // wave order (fixed, so results are deterministic) and writes them (to C, or with
   // split-K to this split's fp32 partial in the uncached scratch) ----
-  float* const red = reinterpret_cast<float*>(lds);
+  float* const red = reinterpret_cast<float*>(lds) + grp * (REDB / 4);  // this tile's
   const int r_out = tid / (TC / 4), c_out = 4 * (tid % (TC / 4));  // for tid < 4*TC
   auto write_c = [&](int rb, float4_t v) {
     const int row = r_out + 16 * rb;
@@ -576,7 +588,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
       else *reinterpret_cast<float4_t*>(partial_at(z, rb)) = v;
     }
   }
-  if (S > 1) {
+  if (G == 1 && S > 1) {
     // hand-off: each thread's partial stores complete before the workgroup barrier;
     // the tile's counter is bumped after it; the last split to arrive adds all splits'
     // partials in split order (bit-identical whichever arrives last), writes C and
@@ -589,7 +601,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
     if (tid == 0) arrived = __hip_atomic_fetch_add(a.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     __syncthreads();
     if (arrived != (uint32_t)S) {
-      sp.store(a.spans, NW, wave, lane);
+      sp.store(a.spans, NW * G, wall, lane);
       return;
     }
     if (tid == 0) __hip_atomic_store(a.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -614,7 +626,7 @@ __global__ __launch_bounds__(64 * NW) void sm24_decode_kernel(const void* B_, co
       for (int rb = 0; rb < RB; rb++) write_c(rb, v[rb]);
     }
   }
-  sp.store(a.spans, NW, wave, lane);
+  sp.store(a.spans, NW * G, wall, lane);
 }
 
 }  // namespace sm24

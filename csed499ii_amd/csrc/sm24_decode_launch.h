@@ -30,11 +30,12 @@ inline size_t static_lds(const void* fn) {
 // MARLIN_HIP_DECODE_RES=0 turns it off.
 constexpr size_t kDecodeLdsMax = 64 * 1024;
 constexpr size_t kCuLds = 160 * 1024;  // LDS of one gfx950 compute unit
-template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP>
+template <int TC, int NW, int MB, bool GROUPED, int VF, int MF, bool DEEP, int G = 1>
 void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
   const int ntiles = a.N / TC;
-  const dim3 grid(a.tail_from > 0 ? a.tail_from + (ntiles - a.tail_from) * a.splits : ntiles * a.splits);
-  const dim3 block(64 * NW);
+  const dim3 grid(G > 1 ? ntiles / G
+                        : a.tail_from > 0 ? a.tail_from + (ntiles - a.tail_from) * a.splits : ntiles * a.splits);
+  const dim3 block(64 * NW * G);
   if constexpr (MB >= 16) {
     // 16 and 32 padded rows: the LDS-DMA kernel (sm24_decode_dma.h).  Its activation
     // pieces travel with each stage into LDS; against the register-ring kernel with
@@ -49,15 +50,15 @@ void launch_decode_v(const GemmArgs& a, int cus, hipStream_t stream) {
     const int nst_max = a.tail_from > 0 ? nst_all : (nst_all + a.splits - 1) / a.splits;
     const size_t dyn = (size_t)MB * ((size_t)nst_max * ks * 64 + 16);
     static const size_t stat =
-        static_lds(reinterpret_cast<const void*>(&sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>));
+        static_lds(reinterpret_cast<const void*>(&sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true, G>));
     const bool fits = stat <= kCuLds && dyn <= kCuLds - stat &&
                       (stat + dyn <= kDecodeLdsMax || (cus > 0 && grid.x <= (unsigned)cus));
     if (forced_res == 1 && nst_max >= 8 && fits) {
-      hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true>), grid, block, dyn, stream,
+      hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, true, G>), grid, block, dyn, stream,
                          a.B, a.meta, a.s, a.A, a.zeros, a.M, a.N, a.K, a.splits, a);
       return;
     }
-    hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false>), grid, block, 0, stream,
+    hipLaunchKernelGGL((sm24_decode_kernel<TC, NW, MB, GROUPED, VF, MF, DEEP, false, G>), grid, block, 0, stream,
                        a.B, a.meta, a.s, a.A, a.zeros, a.M, a.N, a.K, a.splits, a);
   }
 }
@@ -88,6 +89,14 @@ void launch_decode_nw(const GemmArgs& a, int mb, bool deep, int vf, int mf, int 
 template <int TC, bool GROUPED>
 hipError_t launch_decode_t(const GemmArgs& a, const DecodeShape& d, int vf, int mf, hipStream_t stream) {
   const int mb = d.mb >= decode_batch(a.M) ? d.mb : decode_batch(a.M);
+  if constexpr (TC == 16) {
+    // three tiles per workgroup (decode_shape sets g = 3 only for these operands)
+    if (d.g == 3 && d.nw == 4 && !d.deep && vf == VAL4 && mf == META4 && (mb == 1 || mb == 4)) {
+      if (mb == 1) launch_decode_v<16, 4, 1, GROUPED, VAL4, META4, false, 3>(a, d.cus, stream);
+      else launch_decode_v<16, 4, 4, GROUPED, VAL4, META4, false, 3>(a, d.cus, stream);
+      return hipGetLastError();
+    }
+  }
   if (d.nw == 4) launch_decode_nw<TC, 4, GROUPED>(a, mb, d.deep, vf, mf, d.cus, stream);
   else launch_decode_nw<TC, 8, GROUPED>(a, mb, d.deep, vf, mf, d.cus, stream);
   return hipGetLastError();

@@ -744,12 +744,22 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   }
   d.deep = decode_deep(K, d.tail_from > 0 ? 1 : d.splits);
   d.cus = cus;
+  // Three 16-column tiles per workgroup of 12 waves where that makes one workgroup per
+  // CU (unsplit, up to 4 rows, the tiles a multiple of 8 XCDs x 4 tiles per chunk x 3):
+  // the workgroup copies its resident activation rows once instead of three times,
+  // and no workgroup's copy queues behind another's weight stream on the CU.
+  // MARLIN_HIP_DECODE_G = 1 keeps one tile per workgroup.
+  static const int forced_g = env_choice("MARLIN_HIP_DECODE_G", {1, 3}, 3);
+  if (forced_g == 3 && d.tc == 16 && d.nw == 4 && d.splits == 1 && d.tail_from == 0 && !d.deep &&
+      decode_batch(M) <= 4 && (d.mb == 0 || d.mb <= 4) && ntiles % 96 == 0 && cus > 0 && ntiles / 3 <= cus)
+    d.g = 3;
   return d;
 }
 
 // Workgroups of a decode launch.
 int decode_workgroups(int N, const DecodeShape& d) {
   const int ntiles = N / d.tc;
+  if (d.g > 1) return ntiles / d.g;
   return d.tail_from > 0 ? d.tail_from + (ntiles - d.tail_from) * d.splits : ntiles * d.splits;
 }
 
@@ -872,7 +882,7 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
     // the 16- and 32-row batches run the LDS-DMA decode kernel
     if ((d.mb > decode_batch(mc) ? d.mb : decode_batch(mc)) >= 16) out[0] = KERNEL_DECODE_DMA;
     out[1] = decode_workgroups(N, d);
-    out[2] = 64 * d.nw;
+    out[2] = 64 * d.nw * d.g;
     out[3] = d.splits;
     out[4] = (M + kDecodeMaxM - 1) / kDecodeMaxM;
   } else if (kernel == KERNEL_PREFILL) {

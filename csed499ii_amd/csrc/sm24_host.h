@@ -54,6 +54,7 @@ struct DecodeShape {
   bool deep;          // register ring: deep (more stages in flight) or 16 VGPRs
   int tail_from = 0;  // > 0: only the tiles from this one are split (tail split)
   int cus = 0;        // compute units the grid runs on (LDS budget of resident rows)
+  int g = 1;          // tiles per workgroup (3: three 16-column tiles sharing resident rows)
 };
 
 // Padded batch of the decode kernel for M rows: 1, 4, 8, 16 or 32.
