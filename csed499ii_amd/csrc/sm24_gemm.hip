@@ -629,7 +629,17 @@ int env_choice(const char* name, std::initializer_list<int> allowed, int fallbac
 // MARLIN_HIP_DECODE_TC / _WAVES / _SPLITS / _DEEP override.
 
 bool decode_deep(int K, int splits);
-DecodeShape decode_shape(int M, int N, int K, int cus) {
+
+// Whether ntiles 16-column tiles can run three to a workgroup of 12 waves: a multiple
+// of 8 XCDs x 4 tiles per 64-column chunk x 3, in at most one workgroup per CU.
+// MARLIN_HIP_DECODE_G = 1 keeps one tile per workgroup.
+bool decode_g3_fits(int ntiles, int cus) {
+  static const int forced_g = env_choice("MARLIN_HIP_DECODE_G", {1, 3}, 3);
+  return forced_g == 3 && ntiles % 96 == 0 && cus > 0 && ntiles / 3 <= cus;
+}
+
+// four_bit: 4-bit values and metadata (the three-tile workgroups exist for those only).
+DecodeShape decode_shape(int M, int N, int K, int cus, bool four_bit) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   static const int forced_splits = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
@@ -701,8 +711,11 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
     // 3-4 rows (the padded batch of 4) on 64-column tiles of 8 waves, as 5-8 rows,
     // where those tiles fill three quarters of the CUs: 7B qkv 4096x12288 at M = 4
     // 7.47 / 7.39 -> 7.14 us (forced sweep, one box); at 1-2 rows the 16-column tiles
-    // stay faster (M = 2: 6.83 against 7.09 us)
-    d = M >= 3 && 4 * (N / 64) >= 3 * cus ? DecodeShape{64, 8, 1} : DecodeShape{16, 4, 1};
+    // stay faster (M = 2: 6.83 against 7.09 us).  Where the 16-column tiles run three
+    // to a workgroup (below) they are faster at 3-4 rows too: 7B qkv at M = 4 6.89 ->
+    // 6.55 us (A/B, same box, two runs each).
+    const bool g3 = four_bit && decode_g3_fits(N / 16, cus);
+    d = M >= 3 && 4 * (N / 64) >= 3 * cus && !g3 ? DecodeShape{64, 8, 1} : DecodeShape{16, 4, 1};
   }
   if (mid && d.mb == 0) d.mb = 16;  // the rest keep the 16-row batch
   if (forced_tc) d.tc = forced_tc;
@@ -749,9 +762,8 @@ DecodeShape decode_shape(int M, int N, int K, int cus) {
   // the workgroup copies its resident activation rows once instead of three times,
   // and no workgroup's copy queues behind another's weight stream on the CU.
   // MARLIN_HIP_DECODE_G = 1 keeps one tile per workgroup.
-  static const int forced_g = env_choice("MARLIN_HIP_DECODE_G", {1, 3}, 3);
-  if (forced_g == 3 && d.tc == 16 && d.nw == 4 && d.splits == 1 && d.tail_from == 0 && !d.deep &&
-      decode_batch(M) <= 4 && (d.mb == 0 || d.mb <= 4) && ntiles % 96 == 0 && cus > 0 && ntiles / 3 <= cus)
+  if (four_bit && d.tc == 16 && d.nw == 4 && d.splits == 1 && d.tail_from == 0 && !d.deep && decode_batch(M) <= 4 &&
+      (d.mb == 0 || d.mb <= 4) && decode_g3_fits(ntiles, cus))
     d.g = 3;
   return d;
 }
@@ -877,7 +889,7 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
   out[0] = kernel;
   if (kernel == KERNEL_DECODE) {
     const int mc = M < kDecodeMaxM ? M : kDecodeMaxM;
-    DecodeShape d = decode_shape(mc, N, K, sms);
+    DecodeShape d = decode_shape(mc, N, K, sms, true);
     if (noalloc) decode_unsplit(d, K);
     // the 16- and 32-row batches run the LDS-DMA decode kernel
     if ((d.mb > decode_batch(mc) ? d.mb : decode_batch(mc)) >= 16) out[0] = KERNEL_DECODE_DMA;
@@ -951,7 +963,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       d.M = mc;
       d.N = N;
       d.K = K;
-      DecodeShape shape = decode_shape(mc, N, K, sms);
+      DecodeShape shape = decode_shape(mc, N, K, sms, vf == VAL4 && mf == META4);
       if (noalloc) decode_unsplit(shape, K);
       if (shape.splits > 1) {
         const int rows = decode_batch(mc) > 16 ? decode_batch(mc) : 16;

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from csed499ii_amd import marlin, synth
-from tests.gpu_util import assert_close, oracle_gemm, slice_cols, to_cpu
+from tests.gpu_util import REL_MAE, assert_close, oracle_gemm, slice_cols, to_cpu
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -255,6 +255,44 @@ def test_decode_tail_split(M):
     for c0 in (254, 300, 340):
         ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"tail split M={M} chunks {c0}..{c0 + 3}")
+
+
+def test_decode_three_tiles_per_workgroup():
+    """Llama-2-7B qkv 4096x12288 at 1-4 rows: 768 16-column tiles run three to a
+    workgroup of 12 waves (256 workgroups, one per CU), the three sharing the
+    workgroup's resident activation rows, in an XCD-ordered tile map of their own.
+    Every output column matches the oracle (a tile mapped twice or never shows up as
+    a wrong 16-column band), at every M of the padded batches of 1 and 4, with group
+    scales; per-column scales on slices; repeats are bit-identical."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip("the tile counts of this case assume 256 CUs")
+    K, N = 4096, 12288
+    for M in (1, 2, 3, 4):
+        p = marlin.plan_2_4(M, K, N, sms=cus)
+        assert p["kernel"] == "decode" and p["splits"] == 1, (M, p)
+        assert p["workgroups"] == 256 and p["threads"] == 768, (M, p)
+    wt, A4 = _problem(4, N, K, 128, 5150)
+    t = to_cpu(wt)
+    ref = oracle_gemm(A4.cpu().numpy(), t)
+    for M in (1, 2, 3, 4):
+        A = A4[:M].contiguous()
+        C = _run(wt, A)
+        assert torch.equal(_run(wt, A), C), f"repeated calls differ at M={M}"
+        assert_close(C.cpu().numpy(), ref[:M], f"three tiles per workgroup, M={M}")
+        # per 16-column tile as well: a misplaced tile is a small share of the columns
+        Cn = C.cpu().numpy().astype(np.float64).reshape(M, N // 16, 16)
+        rn = ref[:M].astype(np.float64).reshape(M, N // 16, 16)
+        err = np.abs(Cn - rn).mean(axis=(0, 2)) / np.abs(rn).mean()
+        assert err.max() <= 10 * REL_MAE, f"M={M}: tile {int(err.argmax())} off by {err.max():.3e}"
+    wt, A4 = _problem(4, N, K, -1, 5160)
+    t = to_cpu(wt)
+    for M in (1, 4):
+        A = A4[:M].contiguous()
+        C = _run(wt, A)
+        for c0 in (0, 95, 188):
+            r = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+            assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), r, f"g=-1 three tiles M={M} slice {c0}")
 
 
 @pytest.mark.parametrize("M,K,N,splits,wgs", [(1, 4096, 8704, 4, 640), (3, 4096, 8704, 4, 640),
