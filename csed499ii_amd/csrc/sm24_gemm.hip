@@ -671,7 +671,10 @@ DecodeShape decode_shape(int M, int N, int K, int cus, bool four_bit) {
   } else if (narrow) {
     if (M > 16) d = {64, 4, 4};
     else if (longk && M > 4) d = {64, 8, 4};
-    else d = {16, M <= 4 ? 8 : 4, 1};
+    // 8 waves at 2-4 rows and for long K; 4 waves at one row and K < 8192 (7B o
+    // 4096x4096 at M = 1: 4.15 -> 4.05 us, forced, one box, two runs each; at M = 2
+    // 4.23 against 4.29, and 7B down at M = 1 6.23 against 6.99, stay on 8)
+    else d = {16, (M <= 4 && (M > 1 || longk)) ? 8 : 4, 1};
   } else if (longk) {
     // long K at wide N (the Llama-2-70B shapes): unsplit tiles where N alone fills the
     // CUs (the widest N up to 8 rows), K splits of 64-column tiles otherwise; 32-column
