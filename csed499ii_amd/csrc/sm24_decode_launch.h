@@ -86,14 +86,22 @@ void launch_decode_nw(const GemmArgs& a, int mb, bool deep, int vf, int mf, int 
   else launch_decode_mb<TC, NW, 32, GROUPED>(a, deep, vf, mf, cus, stream);
 }
 
+// Three 16-column tiles of 4 waves per workgroup, 1 or 4 padded rows.
+template <bool GROUPED, int VF, int MF>
+void launch_decode_g3(const GemmArgs& a, int mb, int cus, hipStream_t stream) {
+  if (mb == 1) launch_decode_v<16, 4, 1, GROUPED, VF, MF, false, 3>(a, cus, stream);
+  else launch_decode_v<16, 4, 4, GROUPED, VF, MF, false, 3>(a, cus, stream);
+}
+
 template <int TC, bool GROUPED>
 hipError_t launch_decode_t(const GemmArgs& a, const DecodeShape& d, int vf, int mf, hipStream_t stream) {
   const int mb = d.mb >= decode_batch(a.M) ? d.mb : decode_batch(a.M);
   if constexpr (TC == 16) {
-    // three tiles per workgroup (decode_shape sets g = 3 only for these operands)
-    if (d.g == 3 && d.nw == 4 && !d.deep && vf == VAL4 && mf == META4 && (mb == 1 || mb == 4)) {
-      if (mb == 1) launch_decode_v<16, 4, 1, GROUPED, VAL4, META4, false, 3>(a, d.cus, stream);
-      else launch_decode_v<16, 4, 4, GROUPED, VAL4, META4, false, 3>(a, d.cus, stream);
+    // three tiles per workgroup (decode_shape sets g = 3 only for these shapes)
+    if (d.g == 3 && d.nw == 4 && !d.deep && (mb == 1 || mb == 4)) {
+      if (vf == VAL3) launch_decode_g3<GROUPED, VAL3, META4>(a, mb, d.cus, stream);
+      else if (mf == META3) launch_decode_g3<GROUPED, VAL4, META3>(a, mb, d.cus, stream);
+      else launch_decode_g3<GROUPED, VAL4, META4>(a, mb, d.cus, stream);
       return hipGetLastError();
     }
   }

@@ -638,8 +638,7 @@ bool decode_g3_fits(int ntiles, int cus) {
   return forced_g == 3 && ntiles % 96 == 0 && cus > 0 && ntiles / 3 <= cus;
 }
 
-// four_bit: 4-bit values and metadata (the three-tile workgroups exist for those only).
-DecodeShape decode_shape(int M, int N, int K, int cus, bool four_bit) {
+DecodeShape decode_shape(int M, int N, int K, int cus) {
   static const int forced_tc = env_choice("MARLIN_HIP_DECODE_TC", {16, 32, 64}, 0);
   static const int forced_nw = env_choice("MARLIN_HIP_DECODE_WAVES", {4, 8}, 0);
   static const int forced_splits = env_choice("MARLIN_HIP_DECODE_SPLITS", {1, 2, 3, 4}, 0);
@@ -717,8 +716,8 @@ DecodeShape decode_shape(int M, int N, int K, int cus, bool four_bit) {
     // stay faster (M = 2: 6.83 against 7.09 us).  Where the 16-column tiles run three
     // to a workgroup (below) they are faster at 3-4 rows too: 7B qkv at M = 4 6.89 ->
     // 6.55 us (A/B, same box, two runs each).
-    const bool g3 = four_bit && decode_g3_fits(N / 16, cus);
-    d = M >= 3 && 4 * (N / 64) >= 3 * cus && !g3 ? DecodeShape{64, 8, 1} : DecodeShape{16, 4, 1};
+    d = M >= 3 && 4 * (N / 64) >= 3 * cus && !decode_g3_fits(N / 16, cus) ? DecodeShape{64, 8, 1}
+                                                                         : DecodeShape{16, 4, 1};
   }
   if (mid && d.mb == 0) d.mb = 16;  // the rest keep the 16-row batch
   if (forced_tc) d.tc = forced_tc;
@@ -765,7 +764,7 @@ DecodeShape decode_shape(int M, int N, int K, int cus, bool four_bit) {
   // the workgroup copies its resident activation rows once instead of three times,
   // and no workgroup's copy queues behind another's weight stream on the CU.
   // MARLIN_HIP_DECODE_G = 1 keeps one tile per workgroup.
-  if (four_bit && d.tc == 16 && d.nw == 4 && d.splits == 1 && d.tail_from == 0 && !d.deep && decode_batch(M) <= 4 &&
+  if (d.tc == 16 && d.nw == 4 && d.splits == 1 && d.tail_from == 0 && !d.deep && decode_batch(M) <= 4 &&
       (d.mb == 0 || d.mb <= 4) && decode_g3_fits(ntiles, cus))
     d.g = 3;
   return d;
@@ -892,7 +891,7 @@ void describe(int M, int N, int K, int sms, bool noalloc, int out[5]) {
   out[0] = kernel;
   if (kernel == KERNEL_DECODE) {
     const int mc = M < kDecodeMaxM ? M : kDecodeMaxM;
-    DecodeShape d = decode_shape(mc, N, K, sms, true);
+    DecodeShape d = decode_shape(mc, N, K, sms);
     if (noalloc) decode_unsplit(d, K);
     // the 16- and 32-row batches run the LDS-DMA decode kernel
     if ((d.mb > decode_batch(mc) ? d.mb : decode_batch(mc)) >= 16) out[0] = KERNEL_DECODE_DMA;
@@ -966,7 +965,7 @@ int run(int vf, int mf, const void* A, const void* B, const void* meta, void* C,
       d.M = mc;
       d.N = N;
       d.K = K;
-      DecodeShape shape = decode_shape(mc, N, K, sms, vf == VAL4 && mf == META4);
+      DecodeShape shape = decode_shape(mc, N, K, sms);
       if (noalloc) decode_unsplit(shape, K);
       if (shape.splits > 1) {
         const int rows = decode_batch(mc) > 16 ? decode_batch(mc) : 16;

@@ -190,3 +190,33 @@ def test_8row_batch_per_column_scales(M, K, N):
     for c0 in (0, chunks // 2, chunks - 4):
         ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"g=-1 {K}x{N} M={M} slice {c0}")
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_three_tiles_per_workgroup_3bit_paths(M):
+    """Llama-2-7B qkv 4096x12288 at 1-4 rows runs three 16-column tiles per workgroup
+    of 12 waves with 3-bit values and with 3-bit metadata as with 4-bit operands:
+    both are bit-identical to the 4-bit call on the same values, which the oracle
+    checks on column slices."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip("the tile counts of this case assume 256 CUs")
+    K, N = 4096, 12288
+    p = marlin.plan_2_4(M, K, N, sms=cus)
+    assert p["workgroups"] == 256 and p["threads"] == 768, p
+    wt = synth.make_weight(K, N, 23 + M, 128, bits=3, device=DEV)
+    A = synth.make_activation(M, K, 29 + M, device=DEV)
+    C3 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    C4 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    Cm = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
+    B4 = _w3_as_w4(wt["B"])
+    marlin.mul_2_4_w3(A, wt["B"], wt["meta"], C3, wt["s"], _ws(N))
+    marlin.mul_2_4(A, B4, wt["meta"], C4, wt["s"], _ws(N))
+    marlin.mul_2_4_meta3(A, B4, marlin.pack_meta3(wt["meta"].reshape(-1)), Cm, wt["s"], _ws(N))
+    torch.cuda.synchronize()
+    assert torch.equal(C3, C4), "3-bit values differ from the 4-bit call"
+    assert torch.equal(Cm, C4), "3-bit metadata differs from the 4-bit call"
+    t = to_cpu(wt)
+    for c0 in (0, 95, 188):
+        ref = oracle_gemm(A.cpu().numpy(), slice_cols(t, c0, 4))
+        assert_close(C3[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"w3 three tiles M={M} slice {c0}")
