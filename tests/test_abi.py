@@ -123,6 +123,26 @@ def test_plan_without_gpu(built_lib):
     assert marlin.plan_2_4(300, 4096, 768)["kernel"] == "general"  # N % 512 != 0
     with pytest.raises(RuntimeError, match="not compatible"):
         marlin.plan_2_4(16, 1000, 512)
+
+
+def test_plan_three_tiles_per_workgroup(built_lib):
+    """Three 16-column tiles per workgroup of 12 waves where a third of the tiles fits
+    the CUs (one workgroup per CU) and the tiles are a multiple of 96: Llama-2-7B qkv
+    (768 tiles) at 1-4 rows on 256 or 304 CUs; not at 5+ rows (16-row batch or
+    64-column tiles), not where 256 workgroups exceed the CUs, and not for shapes
+    whose tiles are no multiple of 96 (7B o: 256 tiles)."""
+    from csed499ii_amd import marlin
+
+    for sms in (256, 304):
+        for M in (1, 2, 3, 4):
+            p = marlin.plan_2_4(M, 4096, 12288, sms=sms)
+            assert (p["kernel"], p["workgroups"], p["threads"], p["splits"]) == ("decode", 256, 768, 1), (sms, M, p)
+    assert marlin.plan_2_4(5, 4096, 12288, sms=256)["threads"] != 768
+    assert marlin.plan_2_4(1, 4096, 12288, sms=80)["threads"] != 768
+    assert marlin.plan_2_4(4, 4096, 12288, sms=80)["threads"] != 768
+    for M in (1, 2, 4):
+        assert marlin.plan_2_4(M, 4096, 4096, sms=256)["threads"] != 768
+    assert marlin.plan_2_4(1, 4096, 12288, sms=256, noalloc=True)["threads"] == 768  # unsplit anyway
     assert marlin.plan_2_4(0, 4096, 4096)["kernel"] is None
 
 
