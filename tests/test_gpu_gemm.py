@@ -317,10 +317,11 @@ def test_decode_tail_split_shapes(M, K, N, splits, wgs):
     _check(wt, A, C, f"tail split M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (24, 4096, 22016), (16, 4096, 22016)])
+@pytest.mark.parametrize("M,K,N", [(8, 4096, 4096), (2, 4096, 12288), (24, 4096, 22016), (16, 4096, 22016)])
 def test_graph_replay_matches_eager(M, K, N):
     """Captured calls replay the eager result bit for bit: 8 rows on 4096x4096 (one
-    16-column tile per workgroup, unsplit), 24 rows on 4096x22016 (every tile's K
+    16-column tile per workgroup, unsplit), 2 rows on 4096x12288 (three 16-column
+    tiles per workgroup, resident rows), 24 rows on 4096x22016 (every tile's K
     split in two) and 16 rows on it (only the tail tiles past one round over the CUs
     split), both through the capture stream's scratch, which the eager call on that
     stream made first."""
