@@ -295,6 +295,25 @@ def test_decode_three_tiles_per_workgroup():
             assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), r, f"g=-1 three tiles M={M} slice {c0}")
 
 
+@pytest.mark.parametrize("M,K,N,g", [(1, 1024, 12288, 128), (2, 1024, 12288, -1), (4, 512, 12288, 128),
+                                     (3, 256, 12288, 128), (1, 1024, 1536, 128), (1, 4096, 1536, -1),
+                                     (1, 256, 3072, 128)])
+def test_decode_three_tiles_short_k_and_narrow(M, K, N, g):
+    """Three tiles per workgroup beyond the 7B qkv shape: short K (fewer than 8
+    stages, so the activation rows travel with every stage instead of resident, down
+    to a single partial stage at K = 256) and narrow N (1536 / 3072 columns: 32 / 64
+    workgroups), grouped and per-column scales; every column against the oracle,
+    repeats bit-identical."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus == 256:
+        p = marlin.plan_2_4(M, K, N, sms=cus)
+        assert p["threads"] == 768 and p["workgroups"] == N // 48 and p["splits"] == 1, p
+    wt, A = _problem(M, N, K, g, 7000 + M + K + N)
+    C = _run(wt, A)
+    assert torch.equal(_run(wt, A), C), "repeated calls differ"
+    _check(wt, A, C, f"three tiles M={M} {K}x{N} g={g}")
+
+
 @pytest.mark.parametrize("M,K,N,splits,wgs", [(1, 4096, 8704, 4, 640), (3, 4096, 8704, 4, 640),
                                              (5, 4096, 4608, 4, 384), (6, 4096, 17408, 4, 640),
                                              (12, 4096, 16896, 4, 288), (16, 2048, 18432, 4, 384)])
