@@ -192,19 +192,20 @@ def test_8row_batch_per_column_scales(M, K, N):
         assert_close(C[:, 64 * c0:64 * (c0 + 4)].cpu().numpy(), ref, f"g=-1 {K}x{N} M={M} slice {c0}")
 
 
-@pytest.mark.parametrize("M", [1, 2, 4])
-def test_three_tiles_per_workgroup_3bit_paths(M):
+@pytest.mark.parametrize("M,K", [(1, 4096), (2, 4096), (4, 4096), (1, 1024), (4, 512)])
+def test_three_tiles_per_workgroup_3bit_paths(M, K):
     """Llama-2-7B qkv 4096x12288 at 1-4 rows runs three 16-column tiles per workgroup
-    of 12 waves with 3-bit values and with 3-bit metadata as with 4-bit operands:
+    of 12 waves with 3-bit values and with 3-bit metadata as with 4-bit operands
+    (and at K = 512 / 1024, where the activation rows travel with every stage):
     both are bit-identical to the 4-bit call on the same values, which the oracle
     checks on column slices."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if cus != 256:
         pytest.skip("the tile counts of this case assume 256 CUs")
-    K, N = 4096, 12288
+    N = 12288
     p = marlin.plan_2_4(M, K, N, sms=cus)
     assert p["workgroups"] == 256 and p["threads"] == 768, p
-    wt = synth.make_weight(K, N, 23 + M, 128, bits=3, device=DEV)
+    wt = synth.make_weight(K, N, 23 + M + K, 128, bits=3, device=DEV)
     A = synth.make_activation(M, K, 29 + M, device=DEV)
     C3 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
     C4 = torch.full((M, N), float("nan"), dtype=torch.half, device=DEV)
